@@ -1,0 +1,248 @@
+"""Benchmark of the Q4_K / Q6_K MUL_MAT and MUL_MAT_ID path on one MI355X.
+
+Headline (value): HBM GB/s of weight bytes of the batch-1 decode GEMV on the Q6_K output head
+151936 x 2048 (255,252,480 weight bytes), one step = one MUL_MAT including the Q8_K quantization of
+the activation, two weight copies alternated so no step finds its weights in the 256 MB MALL.
+roofline: the GEMV kernel alone (activation already Q8_K), timed with HIP events on the stream it is
+launched on, algorithmic bytes = weight bytes per launch.
+cpu_baseline: the restated iqk AVX-512 VNNI CPU path (oracle/tq_cpu_baseline.c) on the host cores,
+same weight bytes, Q8_K quantization included, median of calls within a bounded budget.
+secondary: the other workloads (Q4_K GEMV 4096 x 4096 batch 1, attention projections, MoE step).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K GEMV HBM GB/s (frac of peak) at batch 1; MoE MUL_MAT_ID µs/token"
+PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-secondary", action="store_true")
+    return p.parse_args()
+
+
+def make_weights(ggml, torch, ty, k, n, copies, seed, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    out = []
+    chunk = max(1, (1 << 27) // k)  # quantize in slices of ~512 MB of fp32
+    for c in range(copies):
+        raw = torch.empty(n * ty.row_size(k), dtype=torch.uint8, device=dev)
+        rb = ty.row_size(k)
+        for r0 in range(0, n, chunk):
+            r1 = min(n, r0 + chunk)
+            src = torch.randn((r1 - r0, k), generator=g, device=dev) * 0.02
+            raw[r0 * rb:r1 * rb] = ggml.quantize(ty, src, r1 - r0, k)
+            del src
+        out.append(ggml.QTensor(ty, (k, n), raw))
+    return out
+
+
+def time_launches(torch, fn, n_launch, reps=3):
+    """Average duration of one launch of fn(i) over n_launch back-to-back launches, with events on
+    the current stream; the best of reps runs."""
+    best = float("inf")
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(n_launch):
+            fn(i)
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e) * 1e3 / n_launch)
+    return best
+
+
+def time_graph(torch, fn, per_graph, replays=20):
+    """Average µs per call of fn(i) captured per_graph times in a HIP graph and replayed."""
+    for i in range(per_graph):  # warm (and allocate any workspace) outside the capture
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per_graph):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e3 / (replays * per_graph)
+
+
+def cpu_baseline(O, np, raw_np, ty_id, k, n, x_np, budget_s):
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or threads))
+    q8 = np.zeros(O.row_size(O.TYPE_Q8_K, k), dtype=np.uint8)
+    y = np.zeros(n, dtype=np.float32)
+    with O.Baseline(threads) as bl:
+        for _ in range(3):
+            bl.mul_mat(ty_id, raw_np, n, k, x_np, q8, y, use_iqk=True)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 64 and (time.perf_counter() < t_end or len(times) < 5):
+            t0 = time.perf_counter()
+            bl.mul_mat(ty_id, raw_np, n, k, x_np, q8, y, use_iqk=True)
+            times.append(time.perf_counter() - t0)
+        iqk = bl.iqk
+    med = statistics.median(times)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return med, threads, len(times), iqk, cpu_model, y
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (multi-GPU sharding is "
+                                   "described in DESIGN.md, not built)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from tetraeder_amd import ggml, _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from tetraeder_amd import build as tq_build
+        tq_build.build()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)}; {_lib.lib().tq_version().decode()}")
+
+    # ---- headline: Q6_K output head 151936 x 2048, batch 1 ----
+    ty, k, n = ggml.Type.Q6_K, 2048, 151936
+    wbytes = n * ty.row_size(k)
+    W = make_weights(ggml, torch, ty, k, n, 2, seed=1, dev=dev)
+    x = torch.randn((1, k), generator=torch.Generator(device=dev).manual_seed(2), device=dev)
+    out = torch.empty((1, n), device=dev)
+    ws = torch.empty(ggml.mul_mat_workspace_size(W[0], x), dtype=torch.uint8, device=dev)
+    step = lambda i: ggml.mul_mat(W[i & 1], x, out=out, workspace=ws)  # noqa: E731
+    log("headline warmup")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    value = wbytes / (ms_per_step * 1e-3) / 1e9
+    log(f"headline {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
+
+    # the GEMV kernel alone: activation already Q8_K, events on the launch stream
+    xq = ggml.QTensor(ggml.Type.Q8_K, (k, 1), ggml.quantize_q8_K(x).view(-1))
+    gemv = lambda i: ggml.mul_mat(W[i & 1], xq, out=out)  # noqa: E731
+    kern_us = time_launches(torch, gemv, 400)
+    kern_us_graph = time_graph(torch, gemv, 64)
+    kern_us = min(kern_us, kern_us_graph)
+    achieved = wbytes / (kern_us * 1e-6) / 1e9
+    log(f"gemv kernel {kern_us:.2f} us -> {achieved:.1f} GB/s")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("gemv_q6_K_151936x2048_m1")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        log("cpu baseline")
+        raw_np = W[0].data.cpu().numpy()
+        x_np = x.cpu().numpy().reshape(-1)
+        med, threads, calls, iqk, cpu_model, y_cpu = cpu_baseline(O, np, raw_np, ty.id, k, n, x_np, args.cpu_seconds)
+        y_gpu = ggml.mul_mat(W[0], x).cpu().numpy().reshape(-1)
+        agree = float(np.abs(y_gpu - y_cpu).max() / np.abs(y_cpu).max())
+        cpu = {"value": round(wbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port", "sample": f"full 151936x2048 Q6_K GEMV incl. Q8_K quantize, median of {calls} calls "
+                                         f"({'AVX-512 VNNI iqk restatement' if iqk else 'scalar vec_dot: no AVX-512 VNNI'}"
+                                         f"; {cpu_model}); max |gpu-cpu| = {agree:.1e} of the largest",
+               "us_per_op": round(med * 1e6, 1)}
+        log(f"cpu {cpu['value']} GB/s on {threads} threads")
+    del W, ws
+    torch.cuda.empty_cache()
+
+    secondary = {}
+    if not args.no_secondary:
+        secondary.update(bench_secondary(ggml, torch, dev))
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: weights N(0,0.02) quantized on device, activations N(0,1)",
+        "config": {"workload": "MUL_MAT Q6_K output head 151936x2048, batch 1 (Q8_K quantize + GEMV), "
+                               "2 rotated weight copies", "n": n, "k": k, "batch": 1, "weight_bytes": wbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_gemv<q6_K,1 col>", "kernel_us": round(kern_us, 2)},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_secondary(ggml, torch, dev):
+    res = {}
+    # Q4_K 4096 x 4096 batch 1: 64 rotated copies (604 MB > 2 x MALL), graph-replayed
+    ty, k, n = ggml.Type.Q4_K, 4096, 4096
+    copies = 64
+    W = make_weights(ggml, torch, ty, k, n, copies, seed=3, dev=dev)
+    x = torch.randn((1, k), device=dev)
+    out = torch.empty((1, n), device=dev)
+    ws = torch.empty(ggml.mul_mat_workspace_size(W[0], x), dtype=torch.uint8, device=dev)
+    xq = ggml.QTensor(ggml.Type.Q8_K, (k, 1), ggml.quantize_q8_K(x).view(-1))
+    wb = n * ty.row_size(k)
+    op_us = time_graph(torch, lambda i: ggml.mul_mat(W[i % copies], x, out=out, workspace=ws), copies)
+    kern_us = time_graph(torch, lambda i: ggml.mul_mat(W[i % copies], xq, out=out), copies)
+    res["q4_K_gemv_4096x4096_m1"] = {"op_us": round(op_us, 2), "gemv_kernel_us": round(kern_us, 2),
+                                     "gemv_GBps": round(wb / kern_us / 1e3, 1),
+                                     "gemv_frac": round(wb / kern_us / 1e3 / PEAK_GBS, 4),
+                                     "op_GBps": round(wb / op_us / 1e3, 1)}
+    log(f"q4_K 4096x4096: {res['q4_K_gemv_4096x4096_m1']}")
+    del W, ws
+    # attention projections (Q4_K), decode batch 1, 4, 16, 32; 16 rotated layer copies
+    shapes = (("q", 2048, 4096), ("k", 2048, 512), ("v", 2048, 512), ("o", 4096, 2048))
+    copies = 16
+    for name, k, n in shapes:
+        W = make_weights(ggml, torch, ty, k, n, copies, seed=n + k, dev=dev)
+        wb = n * ty.row_size(k)
+        for m in (1, 4, 16, 32):
+            x = torch.randn((m, k), device=dev)
+            out = torch.empty((m, n), device=dev)
+            ws = torch.empty(ggml.mul_mat_workspace_size(W[0], x), dtype=torch.uint8, device=dev)
+            us = time_graph(torch, lambda i: ggml.mul_mat(W[i % copies], x, out=out, workspace=ws), copies)
+            res[f"attn_{name}_proj_{k}x{n}_m{m}"] = {"op_us": round(us, 2), "GBps": round(wb / us / 1e3, 1)}
+        del W
+        log(f"attn {name}: " + ", ".join(f"m{m} {res[f'attn_{name}_proj_{k}x{n}_m{m}']['op_us']}us" for m in (1, 4, 16, 32)))
+    torch.cuda.empty_cache()
+    return res
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+/*
+ * tq.h -- C ABI of the MI355X (gfx950) Q4_K / Q6_K matmul library (libtq.so).
+ *
+ * The library replaces, for the Q4_K and Q6_K weight types, what ggml's GPU backend does for the two
+ * graph operators the Tetraeder engine emits for every quantized weight matmul:
+ *
+ *   MUL_MAT     Context::mul_mat(a, b)          crates/ggml-sys/src/ggml/context.rs:294-299
+ *   MUL_MAT_ID  Context::mul_mat_id(as, b, ids) crates/ggml-sys/src/ggml/context.rs:320-336
+ *
+ * with ggml's tensor semantics (ne = elements per dimension, nb = byte strides, dimension 0 fastest),
+ * the Q8_K activation quantization ggml applies to src1 (quantize_row_q8_K, called by the reference at
+ * crates/ggml-sys/tests/iqk_kernels.rs:52,64) and patch 0004's rule that a negative expert id reads no
+ * weights and yields an exact zero row (patches/0004-cuda-mul-mat-id-skip-negative.patch:1-10).
+ *
+ * Conventions (crates/ggml-sys/src/ggml/mod.rs:3-41, sched.rs:112-127, backend.rs:262-280):
+ *   - every compute entry point is asynchronous on the caller's HIP stream (a hipStream_t passed as
+ *     void *; NULL is the null stream) and never synchronizes the host; ids stay on the device;
+ *   - every pointer in a tq_tensor and every workspace is device memory owned by the caller;
+ *   - return codes mirror enum ggml_status: 0 success, -1 failed (invalid arguments or an unsupported
+ *     case; tq_last_error() says which), -2 allocation failed;
+ *   - the workspace is caller-provided device memory of at least the size the matching
+ *     *_workspace_size() reports (a graph-capture-safe arena); workspace == NULL makes the library use
+ *     a grow-only per-device buffer of its own (allocates on growth, so not capture-safe).
+ *
+ * There is no CPU fallback inside this library: an unsupported case returns -1 and the caller keeps
+ * ggml's own backend for it, as ggml's supports_op contract does.
+ */
+#ifndef TQ_H
+#define TQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Tensor type ids are ggml's enum ggml_type values (also the GGUF tensor type ids). */
+enum tq_type {
+    TQ_TYPE_F32 = 0,
+    TQ_TYPE_Q4_K = 12,  /* 144 bytes per 256 weights */
+    TQ_TYPE_Q6_K = 14,  /* 210 bytes per 256 weights */
+    TQ_TYPE_Q8_K = 15,  /* 292 bytes per 256 values (activations) */
+    TQ_TYPE_I32 = 26,
+};
+
+/* Operator ids for tq_supports_op; the ggml-side wrapper maps GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID. */
+enum tq_op {
+    TQ_OP_MUL_MAT = 1,
+    TQ_OP_MUL_MAT_ID = 2,
+};
+
+enum tq_status {
+    TQ_STATUS_SUCCESS = 0,
+    TQ_STATUS_FAILED = -1,
+    TQ_STATUS_ALLOC_FAILED = -2,
+};
+
+/* A view of a ggml tensor in device memory: struct ggml_tensor's type, ne[4], nb[4] and data. */
+typedef struct tq_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t nb[4];
+    void *data;
+} tq_tensor;
+
+/* Message of the last failed call on this host thread ("" when none). */
+const char *tq_last_error(void);
+
+/* Library version, for the loader's log line. */
+const char *tq_version(void);
+
+/* 1 when MUL_MAT (op TQ_OP_MUL_MAT) or MUL_MAT_ID (TQ_OP_MUL_MAT_ID) of src0 type type_a against
+ * src1 type type_b runs here; 0 means the caller keeps ggml's backend for that node.
+ * Replaces ggml_backend_dev_supports_op for these nodes (ggml-backend.h; the module registry loaded at
+ * crates/ggml-sys/src/llama/mod.rs:191-231). */
+int tq_supports_op(int op, int type_a, int type_b);
+
+/* Q8_K quantization of src (F32, ne[0] a multiple of 256, any row strides nb[1..3]) into dst as
+ * contiguous blocks: row r = ((i3*ne2 + i2)*ne1 + i1) occupies bytes [r*ne0/256*292, ...).
+ * Bit-identical to ggml's quantize_row_q8_K(_ref) (ggml-quants.c at b12426; the reference calls it at
+ * crates/ggml-sys/tests/iqk_kernels.rs:52,64), except that an all-zero block's bsums are written as 0
+ * where ggml leaves them unwritten. */
+int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream);
+
+/* Workspace bytes tq_mul_mat needs for these operands (the Q8_K copy of an F32 b; 0 for a Q8_K b). */
+size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b);
+
+/* dst = MUL_MAT(a, b), ggml semantics: a Q4_K/Q6_K [K, N, ne02, ne03], b F32 [K, M, ne12, ne13]
+ * (or b already Q8_K, contiguous, which is used as is, as ggml-cpu does when src1 has vec_dot_type),
+ * dst F32 [N, M, ne12, ne13], a broadcast over dims 2 and 3 (ne12 % ne02 == 0, ne13 % ne03 == 0);
+ * dst[n, m, i2, i3] = sum_k a[k, n, i2/(ne12/ne02), i3/(ne13/ne03)] * q8k(b[:, m, i2, i3])[k].
+ * Replaces the GPU backend's MUL_MAT for Context::mul_mat (crates/ggml-sys/src/ggml/context.rs:294-299),
+ * run by Sched::compute / Backend::compute_async (sched.rs:112, backend.rs:262). */
+int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
+               void *stream);
+
+/* Workspace bytes tq_mul_mat_id needs for these operands. */
+size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids);
+
+/* dst = MUL_MAT_ID(as, b, ids), ggml semantics: as Q4_K/Q6_K [K, N, n_expert] (stacked expert slots,
+ * raw GGUF slabs), b F32 [K, ne11, T] with ne11 == 1 or ne11 == n_used, ids I32 [n_used, T],
+ * dst F32 [N, n_used, T]; dst[:, j, t] = as[:, :, ids[j, t]] . q8k(b[:, j % ne11, t]).
+ * ids[j, t] < 0 reads no weights and writes an exact zero row (patch 0004,
+ * patches/0004-cuda-mul-mat-id-skip-negative.patch:116-137,214-253); ids >= n_expert are undefined
+ * behaviour in ggml and are written as zero rows here. Each expert's weights are read once per call
+ * for all the tokens routed to it; the routing is compacted on the device (no host copy of ids,
+ * unlike the generic path at patches/0004:12-79). Replaces the GPU backend's MUL_MAT_ID for
+ * Context::mul_mat_id (crates/ggml-sys/src/ggml/context.rs:320-336). */
+int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
+                  size_t workspace_size, void *stream);
+
+/* Dequantize n elements of type (Q4_K, Q6_K or Q8_K; n a multiple of 256) from src to F32 dst.
+ * Replaces ggml_get_type_traits(ty)->to_float as used by quant::to_f32
+ * (crates/ggml-sys/src/ggml/quant.rs:20-48) for device buffers. */
+int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream);
+
+/* Quantize nrows rows of n_per_row F32 values (contiguous, device) to Q4_K or Q6_K blocks (device).
+ * The device counterpart of quant::quantize (crates/ggml-sys/src/ggml/quant.rs:54-101): a one-pass
+ * scale/min fit per sub-block, not ggml's iterative search, so the bytes differ from ggml's while
+ * every block is valid; for model conversion and synthetic weights, never on the matmul path. */
+int tq_quantize_weights(int type, const float *src, void *dst, int64_t nrows, int64_t n_per_row, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_H */

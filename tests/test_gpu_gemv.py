@@ -1,0 +1,168 @@
+"""MUL_MAT (decode GEMV, 1..32 columns) on the GPU against the oracle's vec_dot on the same bytes.
+
+Bar: every output within 1e-3 of the largest reference magnitude (the fp32 accumulation-order
+tolerance) and within the per-output f64 bound 1e-5 * sum|w x| + 1e-6 of
+crates/ggml-sys/tests/iqk_kernels.rs:127-148. Weights come from the device quantizer (N(0, 0.02)),
+activations are N(0, 1); the bytes are copied back so both sides consume the same input.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tetraeder_amd import ggml
+from tests.helpers import normal
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+TYPES = {"q4_K": ggml.Type.Q4_K, "q6_K": ggml.Type.Q6_K}
+
+
+def _case(name):
+    print(f"[gemv] {name}", file=sys.stderr, flush=True)
+
+
+def make_weights(ty, k, n, ne2, seed, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    src = torch.randn((ne2 * n, k), generator=g, device=device) * 0.02
+    raw = ggml.quantize(ty, src, ne2 * n, k)
+    return ggml.QTensor(ty, (k, n, ne2), raw)
+
+
+def check(got, want, what, bound=None, ref=None):
+    scale = max(float(np.abs(want).max()), 1e-6)
+    worst = float(np.abs(got.astype(np.float64) - want).max() / scale)
+    assert worst <= TOL, f"{what}: worst {worst:.2e} of the largest > {TOL:.0e}"
+    if bound is not None:
+        excess = np.abs(got.astype(np.float64) - ref) - bound
+        assert np.all(excess <= 0), f"{what}: above the f64 bound by {excess.max():.3e}"
+    return worst
+
+
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+@pytest.mark.parametrize("k", [256, 512, 768, 2048, 4096])
+@pytest.mark.parametrize("n", [1, 5, 96, 1031])
+def test_gemv_one_column(gpu, tname, k, n):
+    _case(f"{tname} k={k} n={n} m=1")
+    ty = TYPES[tname]
+    w = make_weights(ty, k, n, 1, seed=k * 31 + n, device=gpu)
+    x = normal((1, k), k + n)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    raw = w.data.cpu().numpy()
+    want = O.mul_mat(ty.id, raw, k, n, x)[0]
+    ref, bound = O.ref_f64(ty.id, raw, k, x[0])
+    check(y[0], want[0], f"{tname} k={k} n={n}", bound, ref)
+
+
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 9, 16, 17, 32])
+def test_gemv_columns(gpu, tname, m):
+    _case(f"{tname} m={m}")
+    ty = TYPES[tname]
+    k, n = 2048, 300
+    w = make_weights(ty, k, n, 1, seed=m, device=gpu)
+    x = normal((m, k), 100 + m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"{tname} m={m}")
+
+
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+def test_gemv_broadcast_and_strides(gpu, tname):
+    """a [K, N, 2] broadcast over b [K, M, 4] (i02 = i12 / 2); b rows strided; dst a strided view."""
+    _case(f"{tname} broadcast")
+    ty = TYPES[tname]
+    k, n, m = 512, 40, 3
+    w = make_weights(ty, k, n, 2, seed=5, device=gpu)
+    xb = normal((4, m, k + 64), 6)
+    xt = torch.from_numpy(xb).to(gpu)[:, :, 32:32 + k]
+    out_big = torch.full((4, m, n + 8), float("nan"), device=gpu)
+    out = out_big[:, :, :n]
+    ggml.mul_mat(w, xt, out=out)
+    got = out_big.cpu().numpy()
+    assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 32:32 + k]), ne2=2)
+    check(got[:, :, :n], want, f"{tname} broadcast")
+
+
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+def test_gemv_golden(gpu, tname):
+    _case(f"{tname} golden")
+    g = np.load(os.path.join(GOLDEN, f"gemv_{tname}.npz"))
+    k, n = int(g["k"]), int(g["n"])
+    w = ggml.QTensor(TYPES[tname], (k, n), torch.from_numpy(g["w"]).to(gpu))
+    y = ggml.mul_mat(w, torch.from_numpy(g["x"]).to(gpu)).cpu().numpy()
+    check(y, g["y"], f"{tname} golden")
+
+
+def test_workspace_argument(gpu):
+    _case("workspace")
+    ty = ggml.Type.Q4_K
+    w = make_weights(ty, 1024, 64, 1, seed=7, device=gpu)
+    x = torch.from_numpy(normal((3, 1024), 8)).to(gpu)
+    need = ggml.mul_mat_workspace_size(w, x)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    a = ggml.mul_mat(w, x, workspace=ws)
+    b = ggml.mul_mat(w, x)
+    assert torch.equal(a, b)
+    with pytest.raises(ggml.Compute):
+        ggml.mul_mat(w, x, workspace=ws[: need // 2])
+
+
+def test_dequantize_matches_oracle(gpu):
+    _case("to_f32")
+    for ty in (ggml.Type.Q4_K, ggml.Type.Q6_K):
+        w = make_weights(ty, 1024, 16, 1, seed=9, device=gpu)
+        got = ggml.to_f32(ty, w.data, 1024 * 16).cpu().numpy()
+        want = O.dequantize(ty.id, w.data.cpu().numpy(), 1024 * 16)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_device_quantizer_round_trip(gpu):
+    """The device weight quantizer writes valid blocks whose round-trip error shrinks with bits
+    (crates/ggml-sys/src/ggml/quant.rs:114-130)."""
+    _case("quantizer round trip")
+    src = torch.randn((64, 2048), device=gpu) * 0.02
+    errs = []
+    for ty in (ggml.Type.Q4_K, ggml.Type.Q6_K):
+        raw = ggml.quantize(ty, src, 64, 2048)
+        back = torch.from_numpy(O.dequantize(ty.id, raw.cpu().numpy(), 64 * 2048)).to(gpu).view(64, 2048)
+        rel = float(((back - src).pow(2).mean() / src.pow(2).mean()).sqrt())
+        errs.append(rel)
+    assert errs[0] < 0.15 and errs[1] < 0.05 and errs[1] < errs[0], errs
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_q6_K_output_head_full_size(gpu, m):
+    """The Q6_K output head 151936 x 2048 at its real size; a seeded sample of 2048 rows against the
+    oracle (the whole matrix is 255 MB)."""
+    _case(f"q6_K head m={m}")
+    ty = ggml.Type.Q6_K
+    k, n = 2048, 151936
+    w = make_weights(ty, k, n, 1, seed=1234, device=gpu)
+    x = normal((m, k), 4321 + m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    rows = np.sort(np.random.default_rng(0).choice(n, 2048, replace=False))
+    rb = ty.row_size(k)
+    sub = w.data.view(n, rb)[torch.from_numpy(rows).to(gpu)].cpu().numpy().reshape(-1)
+    want = O.mul_mat(ty.id, sub, k, len(rows), x)[0]
+    check(y[:, rows], want, f"q6_K head m={m}")
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 32])
+def test_attention_projections(gpu, m):
+    """q_proj 2048->4096, k/v_proj 2048->512, o_proj 4096->2048, Q4_K, at decode batch m."""
+    ty = ggml.Type.Q4_K
+    for name, k, n in (("q", 2048, 4096), ("k", 2048, 512), ("v", 2048, 512), ("o", 4096, 2048)):
+        _case(f"attn {name} m={m}")
+        w = make_weights(ty, k, n, 1, seed=n + k + m, device=gpu)
+        x = normal((m, k), m + k)
+        y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+        want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+        check(y, want, f"{name}_proj m={m}")

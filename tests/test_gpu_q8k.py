@@ -1,0 +1,82 @@
+"""Q8_K activation quantization on the GPU is bit-identical to the oracle (ggml's quantize_row_q8_K):
+d, every qs byte and every bsum, over seeded inputs with ties, zero blocks, extreme magnitudes and
+non-contiguous or misaligned rows. Compares against the committed golden fixture too."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tetraeder_amd import ggml
+from tests.helpers import normal, xorshift_noise
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "q8k_vectors.npz")
+
+
+def _case(name):
+    print(f"[q8k] {name}", file=sys.stderr, flush=True)
+
+
+def _inputs(kind, rows, k, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        return normal((rows, k), seed)
+    if kind == "noise":
+        return xorshift_noise(rows * k, seed).reshape(rows, k)
+    if kind == "ties":  # halves and integers against exact scales: every rounding is a tie case
+        x = rng.integers(-254, 255, size=(rows, k)).astype(np.float32) / 2
+        x[:, ::256] = -127.0
+        return x
+    if kind == "zero_blocks":
+        x = normal((rows, k), seed)
+        x[:, 256:512] = 0.0
+        x[0, :256] = -0.0
+        return x
+    if kind == "dup_max":  # the same |max| several times with both signs
+        x = normal((rows, k), seed)
+        x[:, 3::97] = 9.0
+        x[:, 50::97] = -9.0
+        return x
+    if kind == "extreme":
+        x = normal((rows, k), seed) * np.float32(1e18)
+        x[:, 1::7] *= np.float32(1e-30)
+        return x
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["normal", "noise", "ties", "zero_blocks", "dup_max", "extreme"])
+@pytest.mark.parametrize("rows,k", [(1, 256), (3, 2048), (17, 4096), (64, 768)])
+def test_q8_K_bit_exact(gpu, kind, rows, k):
+    _case(f"{kind} rows={rows} k={k}")
+    x = _inputs(kind, rows, k, seed=rows * 1000 + k)
+    got = ggml.quantize_q8_K(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.quantize_row_q8_K(x).reshape(rows, -1)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_q8_K_strided_and_misaligned_rows(gpu):
+    _case("strided / misaligned")
+    k = 1024
+    wide = torch.from_numpy(normal((5, k + 7), 77)).to(gpu)
+    for view in (wide[:, :k], wide[:, 1:k + 1], wide[:, 3:k + 3]):  # row stride k+7 floats; offsets 0,4,12 B
+        got = ggml.quantize_q8_K(view).cpu().numpy()
+        want = O.quantize_row_q8_K(np.ascontiguousarray(view.cpu().numpy())).reshape(5, -1)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q8_K_batched_4d(gpu):
+    _case("4d")
+    x = normal((2, 3, 4, 512), 78)
+    got = ggml.quantize_q8_K(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.quantize_row_q8_K(x.reshape(-1, 512)).reshape(24, -1)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_q8_K_golden(gpu):
+    _case("golden")
+    g = np.load(GOLDEN)
+    got = ggml.quantize_q8_K(torch.from_numpy(g["x"]).to(gpu)).cpu().numpy()
+    np.testing.assert_array_equal(got, g["q8"])

@@ -1,0 +1,251 @@
+// tq_api.hip -- the C ABI of libtq.so (include/tq.h): argument checks with ggml's shape rules, the
+// Q8_K activation pass, and dispatch to the gfx950 kernels. No host synchronization, no CPU fallback.
+#include "tq.h"
+#include "tq_device.h"
+#include "tq_internal.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+namespace tq {
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+static int check_hip(hipError_t e, const char *what) {
+    if (e == hipSuccess) return TQ_STATUS_SUCCESS;
+    return fail(e == hipErrorOutOfMemory ? TQ_STATUS_ALLOC_FAILED : TQ_STATUS_FAILED, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+constexpr int MAX_DEVICES = 64;
+
+int device_cu_count() {
+    static int cus[MAX_DEVICES] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Grow-only per-device workspace for callers that pass none (allocates on growth: not capture-safe).
+static void *own_workspace(size_t bytes, int *rc) {
+    static std::mutex mu;
+    static void *buf[MAX_DEVICES] = {nullptr};
+    static size_t cap[MAX_DEVICES] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        *rc = fail(TQ_STATUS_FAILED, "no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < bytes) {
+        if (buf[dev]) (void)hipFree(buf[dev]);  // hipFree waits for work that still uses the old buffer
+        buf[dev] = nullptr;
+        cap[dev] = 0;
+        if (hipMalloc(&buf[dev], bytes) != hipSuccess) {
+            *rc = fail(TQ_STATUS_ALLOC_FAILED, "workspace of %zu bytes", bytes);
+            return nullptr;
+        }
+        cap[dev] = bytes;
+    }
+    *rc = TQ_STATUS_SUCCESS;
+    return buf[dev];
+}
+
+static bool is_weight(int t) { return t == TQ_TYPE_Q4_K || t == TQ_TYPE_Q6_K; }
+
+static size_t type_size(int t) {
+    switch (t) {
+    case TQ_TYPE_F32:
+    case TQ_TYPE_I32: return 4;
+    case TQ_TYPE_Q4_K: return Q4K_BYTES;
+    case TQ_TYPE_Q6_K: return Q6K_BYTES;
+    case TQ_TYPE_Q8_K: return Q8K_BYTES;
+    default: return 0;
+    }
+}
+
+static size_t row_size(int t, int64_t ne) {
+    if (is_weight(t) || t == TQ_TYPE_Q8_K) return type_size(t) * (size_t)(ne / QK);
+    return type_size(t) * (size_t)ne;
+}
+
+static int64_t nrows(const tq_tensor *t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+
+static int check_tensor(const tq_tensor *t, const char *name) {
+    if (!t) return fail(TQ_STATUS_FAILED, "%s is NULL", name);
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] < 0) return fail(TQ_STATUS_FAILED, "%s ne[%d] = %lld", name, i, (long long)t->ne[i]);
+    if (!t->data && nrows(t) * t->ne[0] > 0) return fail(TQ_STATUS_FAILED, "%s data is NULL", name);
+    return TQ_STATUS_SUCCESS;
+}
+
+// The weight-side layout the GEMV kernels read: Q4_K blocks 16-byte aligned (header and qs are read as
+// 16-byte words), Q6_K blocks 2-byte aligned (read through aligned dword windows).
+static int check_weight_layout(const tq_tensor *a, const char *name) {
+    if (!is_weight(a->type)) return fail(TQ_STATUS_FAILED, "%s type %d is not Q4_K (12) or Q6_K (14)", name, a->type);
+    if (a->ne[0] % QK) return fail(TQ_STATUS_FAILED, "%s ne[0] = %lld is not a multiple of 256", name, (long long)a->ne[0]);
+    if (a->nb[0] != type_size(a->type)) return fail(TQ_STATUS_FAILED, "%s nb[0] is not the block size", name);
+    if (a->nb[1] < row_size(a->type, a->ne[0])) return fail(TQ_STATUS_FAILED, "%s rows overlap (nb[1])", name);
+    const size_t align = a->type == TQ_TYPE_Q4_K ? 16 : 2;
+    if ((uintptr_t)a->data % align || a->nb[1] % align || a->nb[2] % align || a->nb[3] % align)
+        return fail(TQ_STATUS_FAILED, "%s data and strides must be %zu-byte aligned", name, align);
+    return TQ_STATUS_SUCCESS;
+}
+
+static int check_f32(const tq_tensor *t, const char *name) {
+    if (t->type != TQ_TYPE_F32) return fail(TQ_STATUS_FAILED, "%s type %d is not F32", name, t->type);
+    if (t->nb[0] != 4 || t->nb[1] % 4 || t->nb[2] % 4 || t->nb[3] % 4)
+        return fail(TQ_STATUS_FAILED, "%s must have contiguous float rows (nb[0] == 4)", name);
+    if ((uintptr_t)t->data % 4) return fail(TQ_STATUS_FAILED, "%s data is not float aligned", name);
+    return TQ_STATUS_SUCCESS;
+}
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+const char *tq_last_error(void) { return g_err.c_str(); }
+
+const char *tq_version(void) { return "tq 0.1 gfx950"; }
+
+int tq_supports_op(int op, int type_a, int type_b) {
+    if (op == TQ_OP_MUL_MAT) return is_weight(type_a) && (type_b == TQ_TYPE_F32 || type_b == TQ_TYPE_Q8_K);
+    if (op == TQ_OP_MUL_MAT_ID) return is_weight(type_a) && type_b == TQ_TYPE_F32;
+    return 0;
+}
+
+int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream) {
+    int rc;
+    if ((rc = check_tensor(src, "src")) != 0) return rc;
+    if ((rc = check_f32(src, "src")) != 0) return rc;
+    if (src->ne[0] % QK) return fail(TQ_STATUS_FAILED, "src ne[0] = %lld is not a multiple of 256", (long long)src->ne[0]);
+    if (!dst && nrows(src) * src->ne[0] > 0) return fail(TQ_STATUS_FAILED, "dst is NULL");
+    if ((uintptr_t)dst % 4) return fail(TQ_STATUS_FAILED, "dst must be 4-byte aligned");
+    return check_hip(launch_quantize_q8_K(src->data, src->ne[0], src->ne[1], src->ne[2], src->ne[3], src->nb[1],
+                                          src->nb[2], src->nb[3], dst, (hipStream_t)stream),
+                     "quantize_q8_K launch");
+}
+
+size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b) {
+    (void)a;
+    return b && b->type == TQ_TYPE_F32 ? q8_bytes(b) : 0;
+}
+
+int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
+               void *stream) {
+    int rc;
+    if ((rc = check_tensor(a, "a")) || (rc = check_tensor(b, "b")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if ((rc = check_weight_layout(a, "a")) || (rc = check_f32(dst, "dst"))) return rc;
+    // src1 in F32 is converted to Q8_K first; src1 already in Q8_K (ggml's vec_dot_type) is used as is,
+    // as ggml-cpu does when src1->type == vec_dot_type. A Q8_K src1 must be contiguous.
+    const bool pre_quantized = b->type == TQ_TYPE_Q8_K;
+    if (pre_quantized) {
+        const size_t rs = row_size(TQ_TYPE_Q8_K, b->ne[0]);
+        if (b->ne[0] % QK || b->nb[0] != Q8K_BYTES || b->nb[1] != rs || b->nb[2] != rs * b->ne[1] ||
+            b->nb[3] != rs * b->ne[1] * b->ne[2] || (uintptr_t)b->data % 4)
+            return fail(TQ_STATUS_FAILED, "a Q8_K b must be contiguous 4-byte aligned blocks");
+    } else if ((rc = check_f32(b, "b"))) {
+        return rc;
+    }
+    if (b->ne[0] != a->ne[0]) return fail(TQ_STATUS_FAILED, "a ne[0] %lld != b ne[0] %lld", (long long)a->ne[0], (long long)b->ne[0]);
+    if (a->ne[2] == 0 || a->ne[3] == 0 || b->ne[2] % a->ne[2] || b->ne[3] % a->ne[3])
+        return fail(TQ_STATUS_FAILED, "b dims 2,3 (%lld, %lld) do not broadcast a (%lld, %lld)", (long long)b->ne[2],
+                    (long long)b->ne[3], (long long)a->ne[2], (long long)a->ne[3]);
+    if (dst->ne[0] != a->ne[1] || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3])
+        return fail(TQ_STATUS_FAILED, "dst shape is not [a.ne1, b.ne1, b.ne2, b.ne3]");
+    if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
+    if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
+    const int nb = (int)(a->ne[0] / QK);
+    const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
+    if (nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
+
+    hipStream_t s = (hipStream_t)stream;
+    void *q8 = b->data;
+    if (!pre_quantized) {
+        const size_t need = q8_bytes(b);
+        if (workspace && workspace_size < need)
+            return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
+        q8 = workspace ? workspace : own_workspace(need, &rc);
+        if (!q8) return rc;
+        if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], b->ne[3], b->nb[1],
+                                                 b->nb[2], b->nb[3], q8, s),
+                            "quantize_q8_K launch")))
+            return rc;
+    }
+    GemvArgs g{};
+    g.w = (const uint8_t *)a->data;
+    g.nrows = a->ne[1];
+    g.nb = nb;
+    g.row_stride = (int64_t)a->nb[1];
+    g.w_s2 = (int64_t)a->nb[2];
+    g.w_s3 = (int64_t)a->nb[3];
+    g.r2 = (int32_t)(b->ne[2] / a->ne[2]);
+    g.r3 = (int32_t)(b->ne[3] / a->ne[3]);
+    g.ne12 = (int32_t)b->ne[2];
+    g.nbatch = (int32_t)(b->ne[2] * b->ne[3]);
+    g.q8 = (const uint8_t *)q8;
+    g.q8_cols = (int32_t)b->ne[1];
+    g.dst = (float *)dst->data;
+    g.d_s1 = (int64_t)(dst->nb[1] / 4);
+    g.d_s2 = (int64_t)(dst->nb[2] / 4);
+    g.d_s3 = (int64_t)(dst->nb[3] / 4);
+    for (int64_t c0 = 0; c0 < b->ne[1]; c0 += nc_max) {
+        g.col0 = (int32_t)c0;
+        g.ncols = (int32_t)std::min<int64_t>(nc_max, b->ne[1] - c0);
+        if ((rc = check_hip(launch_gemv(a->type, g, s), "gemv launch"))) return rc;
+    }
+    return TQ_STATUS_SUCCESS;
+}
+
+size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids) {
+    (void)as, (void)b, (void)ids;
+    return 0;
+}
+
+int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
+                  size_t workspace_size, void *stream) {
+    (void)as, (void)b, (void)ids, (void)dst, (void)workspace, (void)workspace_size, (void)stream;
+    return fail(TQ_STATUS_FAILED, "MUL_MAT_ID is not built yet");
+}
+
+int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {
+    if (!is_weight(type) && type != TQ_TYPE_Q8_K) return fail(TQ_STATUS_FAILED, "to_f32: type %d", type);
+    if (n % QK) return fail(TQ_STATUS_FAILED, "to_f32: n = %lld is not a multiple of 256", (long long)n);
+    if (n && (!src || !dst)) return fail(TQ_STATUS_FAILED, "to_f32: NULL buffer");
+    return check_hip(launch_to_f32(type, src, dst, n, (hipStream_t)stream), "to_f32 launch");
+}
+
+int tq_quantize_weights(int type, const float *src, void *dst, int64_t nrows_, int64_t n_per_row, void *stream) {
+    if (!is_weight(type)) return fail(TQ_STATUS_FAILED, "quantize_weights: type %d", type);
+    if (n_per_row <= 0 || n_per_row % QK) return fail(TQ_STATUS_FAILED, "quantize_weights: n_per_row = %lld", (long long)n_per_row);
+    if (nrows_ < 0) return fail(TQ_STATUS_FAILED, "quantize_weights: nrows < 0");
+    if (nrows_ && (!src || !dst)) return fail(TQ_STATUS_FAILED, "quantize_weights: NULL buffer");
+    return check_hip(launch_quantize_weights(type, src, dst, nrows_, n_per_row, (hipStream_t)stream),
+                     "quantize_weights launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// tq_device.h -- block formats and wave64 helpers shared by the gfx950 kernels.
+//
+// Block layouts are ggml's (byte offsets inside one 256-element super-block):
+//   Q4_K 144 B: d f16 @0, dmin f16 @2, scales[12] @4, qs[128] @16
+//               (reference evidence: patches/0002-iqk-avx512-q4k-q6k-decode.patch:371-380,1430-1487)
+//   Q6_K 210 B: ql[128] @0, qh[64] @128, scales[16] i8 @192, d f16 @208 (patches/0002:1638-1663)
+//   Q8_K 292 B: d f32 @0, qs[256] i8 @4, bsums[16] i16 @260 (patches/0002:1277-1294)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tq {
+
+constexpr int QK = 256;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8K_BYTES = 292;
+constexpr int Q8K_QS = 4;
+constexpr int Q8K_BSUMS = 260;
+
+enum Fmt { FMT_Q4K = 12, FMT_Q6K = 14 };
+
+template <int F> struct FmtInfo;
+template <> struct FmtInfo<FMT_Q4K> { static constexpr int bytes = Q4K_BYTES; };
+template <> struct FmtInfo<FMT_Q6K> { static constexpr int bytes = Q6K_BYTES; };
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32: round to nearest even
+}
+
+// v_dot4_i32_i8: c + sum of the four signed byte products of a and b.
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// The 32-bit window starting `shift` bytes into the 64-bit value (hi:lo), shift in 0..3.
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+__device__ __forceinline__ int sext8(uint32_t v, int bit) { return (int)(v << (24 - bit)) >> 24; }
+
+// Butterfly sum over aligned groups of W lanes (W a power of two <= 64): every lane of a group ends
+// with the group's total.
+template <int W> __device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int W> __device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+}  // namespace tq

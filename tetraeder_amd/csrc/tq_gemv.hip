@@ -1,0 +1,243 @@
+// tq_gemv.hip -- decode GEMV over Q4_K / Q6_K weights and Q8_K activations (1..8 columns per launch).
+//
+// The work is HBM-bound: every weight byte is read once and used ncols times. Layout of the work:
+//   - a workgroup of 8 waves stages the launch's Q8_K activation columns in LDS once, re-ordered so
+//     each lane reads the 32 activation bytes that pair with its weights as two 16-byte LDS reads;
+//   - each wave then streams rows: LPR lanes per row (8 lanes per super-block, LPR/8 super-blocks of
+//     a row in flight), 64/LPR rows per wave pass, a contiguous range of passes per wave;
+//   - a lane covers 32 weights of a super-block: Q4_K one 16-byte load of qs plus the 16-byte header,
+//     Q6_K three 8-byte windows (ql, ql+32, qh) and the scale/d tail, read as 4-byte-aligned dwords
+//     that contain the window and re-aligned with v_alignbyte (a Q6_K block is only 2-byte aligned);
+//   - integer sub-block sums with v_dot4_i32_i8, the Q4_K mins and the Q6_K -32 offset folded in
+//     through the Q8_K bsums (the iqk scheme, patches/0002-iqk-avx512-q4k-q6k-decode.patch:1296-1342,
+//     1638-1663, 1713-1722), one fp32 multiply-add per super-block and column;
+//   - the row total is a butterfly over the row's lanes; lane c of a row writes column c.
+// Dword windows never leave the 4-byte words that hold the block's own bytes, so no read crosses into
+// a page the tensor does not touch.
+#include "tq_device.h"
+#include "tq_internal.h"
+
+#include <algorithm>
+
+namespace tq {
+
+constexpr int GEMV_WAVES = 8;
+constexpr int ACT_BS_BYTES = 64;  // per (column, block): 8 lanes x up to 4 int16 bsums
+
+// Where lane u's activation bytes live: 32 bytes per lane, in the order the lane consumes them.
+// Q4_K lane u = 2c + half: [y[64c + 16half + 0..15] | y[64c + 32 + 16half + 0..15]].
+// Q6_K lane u = 4h + v:    [y[128h + 32k + 8v + 0..7] for k = 0..3].
+template <int F> __device__ __forceinline__ int act_perm(int e) {
+    if (F == FMT_Q4K) {
+        const int c = e >> 6, r = e & 63, part = r >> 5, l = r & 31, half = l >> 4, off = l & 15;
+        return (2 * c + half) * 32 + part * 16 + off;
+    } else {
+        const int h = e >> 7, r = e & 127, k = r >> 5, l = r & 31, v = l >> 3, j = l & 7;
+        return (4 * h + v) * 32 + 8 * k + j;
+    }
+}
+
+// bsums slot s of lane u: Q4_K two slots (the lane's 16-element halves of sub-blocks 2c and 2c+1),
+// Q6_K four slots (the 16-element groups its four 8-element windows belong to).
+template <int F> __device__ __forceinline__ int act_bs_src(int u, int s) {
+    if (F == FMT_Q4K) return 4 * (u >> 1) + (u & 1) + 2 * s;
+    return 8 * (u >> 2) + 2 * s + ((u & 3) >> 1);
+}
+
+template <int F, int NC>
+__device__ __forceinline__ void stage_activations(const uint8_t *__restrict__ q8, int nb, int ncols, uint8_t *lds_qs,
+                                                  int16_t *lds_bs, float *lds_d) {
+    const int tid = threadIdx.x;
+    const int nqs = NC * nb * 64;  // dwords of qs
+    for (int i = tid; i < nqs; i += GEMV_WAVES * 64) {
+        const int t = i & 63, cb = i >> 6, c = cb / nb;
+        uint32_t v = 0;
+        if (c < ncols) v = *(const uint32_t *)(q8 + (size_t)cb * Q8K_BYTES + Q8K_QS + 4 * t);
+        *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * t)) = v;
+    }
+    constexpr int SLOTS = F == FMT_Q4K ? 2 : 4;
+    const int nbs = NC * nb * 8 * SLOTS;
+    for (int i = tid; i < nbs; i += GEMV_WAVES * 64) {
+        const int s = i % SLOTS, u = (i / SLOTS) & 7, cb = i / (SLOTS * 8), c = cb / nb;
+        int16_t v = 0;
+        if (c < ncols) v = *(const int16_t *)(q8 + (size_t)cb * Q8K_BYTES + Q8K_BSUMS + 2 * act_bs_src<F>(u, s));
+        lds_bs[cb * (ACT_BS_BYTES / 2) + u * SLOTS + s] = v;
+    }
+    for (int i = tid; i < NC * nb; i += GEMV_WAVES * 64) {
+        lds_d[i] = (i / nb) < ncols ? *(const float *)(q8 + (size_t)i * Q8K_BYTES) : 0.f;
+    }
+}
+
+template <int NC> struct Acc {
+    float v[NC];
+};
+
+// One Q4_K super-block against NC staged columns; lane u = 2c + half covers qs[16u .. 16u+15].
+template <int NC>
+__device__ __forceinline__ void block_q4K(const uint8_t *__restrict__ blk, int u, int b, int nb, const uint8_t *lds_qs,
+                                          const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+    const uint4 hdr = *(const uint4 *)blk;
+    const uint4 qv = *(const uint4 *)(blk + 16 + 16 * u);
+    const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+    const int c = u >> 1;
+    uint32_t scw, mw;
+    if (c < 2) {
+        scw = hdr.y & 0x3f3f3f3fu;
+        mw = hdr.z & 0x3f3f3f3fu;
+    } else {
+        scw = (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u);
+        mw = ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u);
+    }
+    const int sh = (c & 1) * 16;
+    const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
+    const int m_lo = (mw >> sh) & 0xff, m_hi = (mw >> (sh + 8)) & 0xff;
+    const uint32_t lo0 = qv.x & 0x0f0f0f0fu, lo1 = qv.y & 0x0f0f0f0fu, lo2 = qv.z & 0x0f0f0f0fu,
+                   lo3 = qv.w & 0x0f0f0f0fu;
+    const uint32_t hi0 = (qv.x >> 4) & 0x0f0f0f0fu, hi1 = (qv.y >> 4) & 0x0f0f0f0fu,
+                   hi2 = (qv.z >> 4) & 0x0f0f0f0fu, hi3 = (qv.w >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+    for (int col = 0; col < NC; ++col) {
+        const int cb = col * nb + b;
+        const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
+        const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
+        const int slo = dot4(lo3, y0.w, dot4(lo2, y0.z, dot4(lo1, y0.y, dot4(lo0, y0.x, 0))));
+        const int shi = dot4(hi3, y1.w, dot4(hi2, y1.z, dot4(hi1, y1.y, dot4(hi0, y1.x, 0))));
+        const uint32_t bsw = *(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2);
+        const int isum = sc_lo * slo + sc_hi * shi;
+        const int msum = m_lo * (int)(int16_t)(bsw & 0xffffu) + m_hi * (int)(int16_t)(bsw >> 16);
+        acc.v[col] += lds_d[cb] * (d * (float)isum - dmin * (float)msum);
+    }
+}
+
+// One Q6_K super-block against NC staged columns; lane u = 4h + v covers elements
+// 128h + 32k + 8v + 0..7 for k = 0..3 (ql windows at 64h+8v and 64h+32+8v, qh window at 128+32h+8v).
+template <int NC>
+__device__ __forceinline__ void block_q6K(const uint8_t *__restrict__ blk, int u, int b, int nb, const uint8_t *lds_qs,
+                                          const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+    const int h = u >> 2, v = u & 3;
+    const uintptr_t base = (uintptr_t)blk;
+    const uint32_t sh = (uint32_t)(base & 3u);  // 0 or 2: block bases are even
+    const uint32_t *pa = (const uint32_t *)((base + 64 * h + 8 * v) & ~(uintptr_t)3);
+    const uint32_t *pb = (const uint32_t *)((base + 64 * h + 32 + 8 * v) & ~(uintptr_t)3);
+    const uint32_t *ph = (const uint32_t *)((base + 128 + 32 * h + 8 * v) & ~(uintptr_t)3);
+    const uint32_t *pt = (const uint32_t *)((base + 192) & ~(uintptr_t)3);
+    const uint32_t a0 = pa[0], a1 = pa[1], a2 = pa[2];
+    const uint32_t b0 = pb[0], b1 = pb[1], b2 = pb[2];
+    const uint32_t h0 = ph[0], h1 = ph[1], h2 = ph[2];
+    const uint32_t t0 = pt[0], t1 = pt[1], t2 = pt[2], t3 = pt[3], t4 = pt[4];
+    const uint32_t A0 = align_bytes(a1, a0, sh), A1 = align_bytes(a2, a1, sh);
+    const uint32_t B0 = align_bytes(b1, b0, sh), B1 = align_bytes(b2, b1, sh);
+    const uint32_t H0 = align_bytes(h1, h0, sh), H1 = align_bytes(h2, h1, sh);
+    const uint32_t r0 = align_bytes(t1, t0, sh), r1 = align_bytes(t2, t1, sh);
+    const uint32_t r2 = align_bytes(t3, t2, sh), r3 = align_bytes(t4, t3, sh);
+    const float d = half_bits_to_float(t4 >> (8 * sh));
+    const uint32_t s01 = h ? r2 : r0, s23 = h ? r3 : r1;
+    const int pos = 8 * (v >> 1);
+    const int sc0 = sext8(s01, pos), sc1 = sext8(s01, pos + 16), sc2 = sext8(s23, pos), sc3 = sext8(s23, pos + 16);
+    const uint32_t m4 = 0x0f0f0f0fu;
+    const uint32_t q00 = (A0 & m4) | ((H0 & 0x03030303u) << 4), q01 = (A1 & m4) | ((H1 & 0x03030303u) << 4);
+    const uint32_t q10 = (B0 & m4) | ((H0 & 0x0c0c0c0cu) << 2), q11 = (B1 & m4) | ((H1 & 0x0c0c0c0cu) << 2);
+    const uint32_t q20 = ((A0 >> 4) & m4) | (H0 & 0x30303030u), q21 = ((A1 >> 4) & m4) | (H1 & 0x30303030u);
+    const uint32_t q30 = ((B0 >> 4) & m4) | ((H0 >> 2) & 0x30303030u), q31 = ((B1 >> 4) & m4) | ((H1 >> 2) & 0x30303030u);
+    const int even = (v & 1) ? 0 : 1;
+#pragma unroll
+    for (int col = 0; col < NC; ++col) {
+        const int cb = col * nb + b;
+        const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
+        const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
+        const int S0 = dot4(q01, y0.y, dot4(q00, y0.x, 0));
+        const int S1 = dot4(q11, y0.w, dot4(q10, y0.z, 0));
+        const int S2 = dot4(q21, y1.y, dot4(q20, y1.x, 0));
+        const int S3 = dot4(q31, y1.w, dot4(q30, y1.z, 0));
+        const uint2 bsw = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
+        const int corr = sc0 * (int)(int16_t)(bsw.x & 0xffffu) + sc1 * (int)(int16_t)(bsw.x >> 16) +
+                         sc2 * (int)(int16_t)(bsw.y & 0xffffu) + sc3 * (int)(int16_t)(bsw.y >> 16);
+        const int isum = sc0 * S0 + sc1 * S1 + sc2 * S2 + sc3 * S3 - 32 * even * corr;
+        acc.v[col] += (lds_d[cb] * d) * (float)isum;
+    }
+}
+
+template <int F, int NC, int LPR>
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a, int passes_per_wave) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int nb = a.nb;
+    const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
+    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
+    const uint8_t *q8 = a.q8 + ((int64_t)(i3 * a.ne12 + i2) * a.q8_cols + a.col0) * nb * Q8K_BYTES;
+    float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3 + a.col0 * a.d_s1;
+
+    uint8_t *lds_qs = lds;
+    int16_t *lds_bs = (int16_t *)(lds + NC * nb * 256);
+    float *lds_d = (float *)(lds + NC * nb * (256 + ACT_BS_BYTES));
+    stage_activations<F, NC>(q8, nb, a.ncols, lds_qs, lds_bs, lds_d);
+    __syncthreads();
+
+    constexpr int G = LPR / 8;     // super-blocks of a row in flight
+    constexpr int RPW = 64 / LPR;  // rows per wave pass
+    const int lane = lane_id();
+    const int u = lane & 7, gb = (lane % LPR) >> 3, lrow = lane / LPR, lir = lane % LPR;
+    const int64_t wave = (int64_t)blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6);
+    const int64_t npass = (a.nrows + RPW - 1) / RPW;
+    const int64_t p_begin = wave * passes_per_wave;
+    const int64_t p_end = min(npass, p_begin + passes_per_wave);
+    for (int64_t p = p_begin; p < p_end; ++p) {
+        const int64_t row = p * RPW + lrow;
+        Acc<NC> acc;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
+        if (row < a.nrows) {
+            const uint8_t *wrow = w + row * a.row_stride;
+            for (int b = gb; b < nb; b += G) {
+                const uint8_t *blk = wrow + (int64_t)b * FmtInfo<F>::bytes;
+                if (F == FMT_Q4K)
+                    block_q4K<NC>(blk, u, b, nb, lds_qs, lds_bs, lds_d, acc);
+                else
+                    block_q6K<NC>(blk, u, b, nb, lds_qs, lds_bs, lds_d, acc);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
+        if (row < a.nrows) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                if (lir == c && c < a.ncols) dst[c * a.d_s1 + row] = acc.v[c];
+        }
+    }
+}
+
+template <int F, int NC>
+static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
+    int lpr;
+    if (a.nb <= 1) lpr = 8;
+    else if (a.nb <= 2) lpr = 16;
+    else if (a.nb <= 4) lpr = 32;
+    else lpr = 64;
+    const int rpw = 64 / lpr;
+    const int64_t npass = (a.nrows + rpw - 1) / rpw;
+    const int64_t target_waves = (int64_t)device_cu_count() * 16;
+    const int ppw = (int)std::max<int64_t>(1, (npass + target_waves - 1) / target_waves);
+    const int64_t waves = (npass + ppw - 1) / ppw;
+    const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
+    const size_t lds = (size_t)NC * a.nb * (256 + ACT_BS_BYTES + 4);
+    switch (lpr) {
+    case 8: k_gemv<F, NC, 8><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
+    case 16: k_gemv<F, NC, 16><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
+    case 32: k_gemv<F, NC, 32><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
+    default: k_gemv<F, NC, 64><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
+    }
+    return hipGetLastError();
+}
+
+template <int F>
+static hipError_t launch_fmt(const GemvArgs &a, hipStream_t stream) {
+    if (a.ncols <= 1) return launch_nc<F, 1>(a, stream);
+    if (a.ncols <= 2) return launch_nc<F, 2>(a, stream);
+    if (a.ncols <= 4) return launch_nc<F, 4>(a, stream);
+    return launch_nc<F, 8>(a, stream);
+}
+
+hipError_t launch_gemv(int type, const GemvArgs &a, hipStream_t stream) {
+    return type == FMT_Q4K ? launch_fmt<FMT_Q4K>(a, stream) : launch_fmt<FMT_Q6K>(a, stream);
+}
+
+}  // namespace tq

@@ -1,0 +1,44 @@
+// tq_internal.h -- launchers shared between the kernel translation units and the C ABI (tq_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tq {
+
+// Q8_K quantization of rows of k floats. Row r = (i3*ne2 + i2)*ne1 + i1 is read at
+// x + i1*s1 + i2*s2 + i3*s3 (byte strides) and written contiguously at y + r*(k/256)*292.
+hipError_t launch_quantize_q8_K(const void *x, int64_t k, int64_t ne1, int64_t ne2, int64_t ne3, size_t s1, size_t s2,
+                                size_t s3, void *y, hipStream_t stream);
+
+// Device weight quantizer (one-pass fit) and dequantizer.
+hipError_t launch_quantize_weights(int type, const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                                   hipStream_t stream);
+hipError_t launch_to_f32(int type, const void *src, float *dst, int64_t n, hipStream_t stream);
+
+// Batched GEMV over Q8_K activations (1 <= ncols <= 8 per launch, ncols*nb*324 <= gemv_max_lds()).
+struct GemvArgs {
+    const uint8_t *w;    // weights of batch (0,0)
+    int64_t nrows;       // N
+    int32_t nb;          // super-blocks per row (K/256)
+    int64_t row_stride;  // bytes between rows
+    int64_t w_s2, w_s3;  // bytes between weight matrices in dims 2, 3
+    int32_t r2, r3;      // broadcast ratios ne12/ne02, ne13/ne03
+    int32_t ne12;        // batch extent of dim 2
+    int32_t nbatch;      // ne12*ne13 (grid.y)
+    const uint8_t *q8;   // Q8_K rows; column c of batch (i2,i3) at q8 + ((i3*ne12+i2)*q8_cols + c)*nb*292
+    int32_t q8_cols;     // columns per batch in the Q8_K buffer
+    int32_t col0;        // first column of this launch
+    int32_t ncols;       // columns of this launch
+    float *dst;          // dst of batch (0,0), column col0 is dst + col0*d_s1
+    int64_t d_s1, d_s2, d_s3;  // float strides of dst
+};
+hipError_t launch_gemv(int type, const GemvArgs &a, hipStream_t stream);
+constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
+constexpr size_t gemv_max_lds() { return 64 * 1024; }
+
+// Device properties cached per device.
+int device_cu_count();
+
+}  // namespace tq
