@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--only", choices=["gemv", "copy"], default=None,
+                   help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
+                        "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
     return p.parse_args()
 
 
@@ -134,6 +137,15 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}; {_lib.lib().tq_version().decode()}")
+    if args.only == "copy":
+        a = torch.empty(1 << 26, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1.0)
+        for _ in range(args.steps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copied {args.steps} x 256 MiB")
+        return
 
     # ---- headline: Q6_K output head 151936 x 2048, batch 1 ----
     ty, k, n = ggml.Type.Q6_K, 2048, 151936
@@ -143,6 +155,13 @@ def main():
     out = torch.empty((1, n), device=dev)
     ws = torch.empty(ggml.mul_mat_workspace_size(W[0], x), dtype=torch.uint8, device=dev)
     step = lambda i: ggml.mul_mat(W[i & 1], x, out=out, workspace=ws)  # noqa: E731
+    if args.only == "gemv":
+        xq = ggml.QTensor(ggml.Type.Q8_K, (k, 1), ggml.quantize_q8_K(x).view(-1))
+        for i in range(args.steps):
+            ggml.mul_mat(W[i & 1], xq, out=out)
+        torch.cuda.synchronize()
+        log(f"ran {args.steps} GEMV launches")
+        return
     log("headline warmup")
     for i in range(args.warmup):
         step(i)
