@@ -45,19 +45,34 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
 
 __device__ __forceinline__ int sext8(uint32_t v, int bit) { return (int)(v << (24 - bit)) >> 24; }
 
-// Butterfly sum over aligned groups of W lanes (W a power of two <= 64): every lane of a group ends
-// with the group's total.
+// Sum over aligned groups of W lanes (W a power of two <= 64), every lane of a group ends with the
+// group's total. Within 16-lane rows the exchanges are DPP moves (quad_perm, row_half_mirror,
+// row_mirror); across rows gfx950's v_permlane16_swap / v_permlane32_swap; no LDS traffic.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
 template <int W> __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    if (W >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    if (W >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (W >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+    if (W >= 16) v += dpp_f<0x140>(v); // row_mirror
+    if (W >= 32) {
+        const uint32_t x = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        v += __builtin_bit_cast(float, ((threadIdx.x >> 4) & 1) ? r[0] : r[1]);
+    }
+    if (W >= 64) {
+        const uint32_t x = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        v += __builtin_bit_cast(float, ((threadIdx.x >> 5) & 1) ? r[0] : r[1]);
+    }
     return v;
 }
 
-template <int W> __device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 

@@ -72,13 +72,49 @@ template <int NC> struct Acc {
     float v[NC];
 };
 
-// One Q4_K super-block against NC staged columns; lane u = 2c + half covers qs[16u .. 16u+15].
+// The raw words one lane loads for one (row, super-block) item. Loads and arithmetic are split so the
+// next item's loads are in flight while the current item is computed.
+template <int F> struct Item;
+
+// Q4_K lane u = 2c + half covers qs[16u .. 16u+15]: the 16-byte header and one 16-byte qs word.
+template <> struct Item<FMT_Q4K> {
+    uint4 hdr, qv;
+    bool valid;
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, int u) {
+        hdr = *(const uint4 *)blk;
+        qv = *(const uint4 *)(blk + 16 + 16 * u);
+    }
+};
+
+// Q6_K lane u = 4h + v covers elements 128h + 32k + 8v + 0..7, k = 0..3: 8-byte windows of ql at
+// 64h+8v and 64h+32+8v and of qh at 128+32h+8v, plus the scale/d tail at 192..209. A block starts
+// at an even address; every window is read as the aligned dwords that contain it (3 dwords per
+// window, 5 for the tail) and realigned by sh bytes.
+template <> struct Item<FMT_Q6K> {
+    uint32_t a0, a1, a2, b0, b1, b2, h0, h1, h2, t0, t1, t2, t3, t4, sh;
+    bool valid;
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, int u) {
+        const int h = u >> 2, v = u & 3;
+        sh = (uint32_t)((uintptr_t)blk & 3u);
+        const uint8_t *blk0 = blk - sh;  // 4-byte aligned
+        const uint32_t *pa = (const uint32_t *)(blk0 + 64 * h + 8 * v);
+        const uint32_t *pb = (const uint32_t *)(blk0 + 64 * h + 32 + 8 * v);
+        const uint32_t *ph = (const uint32_t *)(blk0 + 128 + 32 * h + 8 * v);
+        const uint32_t *pt = (const uint32_t *)(blk0 + 192);
+        a0 = pa[0], a1 = pa[1], a2 = pa[2];
+        b0 = pb[0], b1 = pb[1], b2 = pb[2];
+        h0 = ph[0], h1 = ph[1], h2 = ph[2];
+        t0 = pt[0], t1 = pt[1], t2 = pt[2], t3 = pt[3], t4 = pt[4];
+    }
+};
+
 template <int NC>
-__device__ __forceinline__ void block_q4K(const uint8_t *__restrict__ blk, int u, int b, int nb, const uint8_t *lds_qs,
-                                          const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
-    const uint4 hdr = *(const uint4 *)blk;
-    const uint4 qv = *(const uint4 *)(blk + 16 + 16 * u);
-    const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+__device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
+                                             const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+    const uint4 hdr = it.hdr, qv = it.qv;
+    // an invalid item read a valid stand-in block; zero scales make its contribution exactly 0
+    const float d = it.valid ? half_bits_to_float(hdr.x) : 0.f;
+    const float dmin = it.valid ? half_bits_to_float(hdr.x >> 16) : 0.f;
     const int c = u >> 1;
     uint32_t scw, mw;
     if (c < 2) {
@@ -97,41 +133,30 @@ __device__ __forceinline__ void block_q4K(const uint8_t *__restrict__ blk, int u
                    hi2 = (qv.z >> 4) & 0x0f0f0f0fu, hi3 = (qv.w >> 4) & 0x0f0f0f0fu;
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
-        const int cb = col * nb + b;
+        const int cb = cb0 + col * nb;
         const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
         const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
         const int slo = dot4(lo3, y0.w, dot4(lo2, y0.z, dot4(lo1, y0.y, dot4(lo0, y0.x, 0))));
         const int shi = dot4(hi3, y1.w, dot4(hi2, y1.z, dot4(hi1, y1.y, dot4(hi0, y1.x, 0))));
         const uint32_t bsw = *(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2);
-        const int isum = sc_lo * slo + sc_hi * shi;
-        const int msum = m_lo * (int)(int16_t)(bsw & 0xffffu) + m_hi * (int)(int16_t)(bsw >> 16);
+        const int isum = mad24(sc_lo, slo, mul24(sc_hi, shi));
+        const int msum = mad24(m_lo, (int)(int16_t)(bsw & 0xffffu), mul24(m_hi, (int)(int16_t)(bsw >> 16)));
         acc.v[col] += lds_d[cb] * (d * (float)isum - dmin * (float)msum);
     }
 }
 
-// One Q6_K super-block against NC staged columns; lane u = 4h + v covers elements
-// 128h + 32k + 8v + 0..7 for k = 0..3 (ql windows at 64h+8v and 64h+32+8v, qh window at 128+32h+8v).
 template <int NC>
-__device__ __forceinline__ void block_q6K(const uint8_t *__restrict__ blk, int u, int b, int nb, const uint8_t *lds_qs,
-                                          const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+__device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
+                                             const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
     const int h = u >> 2, v = u & 3;
-    const uintptr_t base = (uintptr_t)blk;
-    const uint32_t sh = (uint32_t)(base & 3u);  // 0 or 2: block bases are even
-    const uint32_t *pa = (const uint32_t *)((base + 64 * h + 8 * v) & ~(uintptr_t)3);
-    const uint32_t *pb = (const uint32_t *)((base + 64 * h + 32 + 8 * v) & ~(uintptr_t)3);
-    const uint32_t *ph = (const uint32_t *)((base + 128 + 32 * h + 8 * v) & ~(uintptr_t)3);
-    const uint32_t *pt = (const uint32_t *)((base + 192) & ~(uintptr_t)3);
-    const uint32_t a0 = pa[0], a1 = pa[1], a2 = pa[2];
-    const uint32_t b0 = pb[0], b1 = pb[1], b2 = pb[2];
-    const uint32_t h0 = ph[0], h1 = ph[1], h2 = ph[2];
-    const uint32_t t0 = pt[0], t1 = pt[1], t2 = pt[2], t3 = pt[3], t4 = pt[4];
-    const uint32_t A0 = align_bytes(a1, a0, sh), A1 = align_bytes(a2, a1, sh);
-    const uint32_t B0 = align_bytes(b1, b0, sh), B1 = align_bytes(b2, b1, sh);
-    const uint32_t H0 = align_bytes(h1, h0, sh), H1 = align_bytes(h2, h1, sh);
-    const uint32_t r0 = align_bytes(t1, t0, sh), r1 = align_bytes(t2, t1, sh);
-    const uint32_t r2 = align_bytes(t3, t2, sh), r3 = align_bytes(t4, t3, sh);
-    const float d = half_bits_to_float(t4 >> (8 * sh));
-    const uint32_t s01 = h ? r2 : r0, s23 = h ? r3 : r1;
+    const uint32_t sh = it.sh;
+    const uint32_t A0 = align_bytes(it.a1, it.a0, sh), A1 = align_bytes(it.a2, it.a1, sh);
+    const uint32_t B0 = align_bytes(it.b1, it.b0, sh), B1 = align_bytes(it.b2, it.b1, sh);
+    const uint32_t H0 = align_bytes(it.h1, it.h0, sh), H1 = align_bytes(it.h2, it.h1, sh);
+    // scales[4j .. 4j+3] for j = 2h and 2h+1 (this lane's four scales live there)
+    const uint32_t s01 = h ? align_bytes(it.t3, it.t2, sh) : align_bytes(it.t1, it.t0, sh);
+    const uint32_t s23 = h ? align_bytes(it.t4, it.t3, sh) : align_bytes(it.t2, it.t1, sh);
+    const float d = it.valid ? half_bits_to_float(it.t4 >> (8 * sh)) : 0.f;
     const int pos = 8 * (v >> 1);
     const int sc0 = sext8(s01, pos), sc1 = sext8(s01, pos + 16), sc2 = sext8(s23, pos), sc3 = sext8(s23, pos + 16);
     const uint32_t m4 = 0x0f0f0f0fu;
@@ -139,10 +164,11 @@ __device__ __forceinline__ void block_q6K(const uint8_t *__restrict__ blk, int u
     const uint32_t q10 = (B0 & m4) | ((H0 & 0x0c0c0c0cu) << 2), q11 = (B1 & m4) | ((H1 & 0x0c0c0c0cu) << 2);
     const uint32_t q20 = ((A0 >> 4) & m4) | (H0 & 0x30303030u), q21 = ((A1 >> 4) & m4) | (H1 & 0x30303030u);
     const uint32_t q30 = ((B0 >> 4) & m4) | ((H0 >> 2) & 0x30303030u), q31 = ((B1 >> 4) & m4) | ((H1 >> 2) & 0x30303030u);
-    const int even = (v & 1) ? 0 : 1;
+    // the -32 offset enters once per 16-element group, on the even lane of the pair sharing it
+    const int even = (v & 1) ? 0 : -32;
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
-        const int cb = col * nb + b;
+        const int cb = cb0 + col * nb;
         const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
         const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
         const int S0 = dot4(q01, y0.y, dot4(q00, y0.x, 0));
@@ -150,15 +176,16 @@ __device__ __forceinline__ void block_q6K(const uint8_t *__restrict__ blk, int u
         const int S2 = dot4(q21, y1.y, dot4(q20, y1.x, 0));
         const int S3 = dot4(q31, y1.w, dot4(q30, y1.z, 0));
         const uint2 bsw = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
-        const int corr = sc0 * (int)(int16_t)(bsw.x & 0xffffu) + sc1 * (int)(int16_t)(bsw.x >> 16) +
-                         sc2 * (int)(int16_t)(bsw.y & 0xffffu) + sc3 * (int)(int16_t)(bsw.y >> 16);
-        const int isum = sc0 * S0 + sc1 * S1 + sc2 * S2 + sc3 * S3 - 32 * even * corr;
+        const int corr = mad24(sc0, (int)(int16_t)(bsw.x & 0xffffu),
+                               mad24(sc1, (int)(int16_t)(bsw.x >> 16),
+                                     mad24(sc2, (int)(int16_t)(bsw.y & 0xffffu), mul24(sc3, (int)(int16_t)(bsw.y >> 16)))));
+        const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mad24(sc3, S3, mul24(even, corr)))));
         acc.v[col] += (lds_d[cb] * d) * (float)isum;
     }
 }
 
 template <int F, int NC, int LPR>
-__global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a, int passes_per_wave) {
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = a.nb;
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
@@ -172,36 +199,57 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a, int passes
     stage_activations<F, NC>(q8, nb, a.ncols, lds_qs, lds_bs, lds_d);
     __syncthreads();
 
-    constexpr int G = LPR / 8;     // super-blocks of a row in flight
+    constexpr int G = LPR / 8;     // super-blocks of a row in flight per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     const int lane = lane_id();
     const int u = lane & 7, gb = (lane % LPR) >> 3, lrow = lane / LPR, lir = lane % LPR;
     const int64_t wave = (int64_t)blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * GEMV_WAVES;
     const int64_t npass = (a.nrows + RPW - 1) / RPW;
-    const int64_t p_begin = wave * passes_per_wave;
-    const int64_t p_end = min(npass, p_begin + passes_per_wave);
-    for (int64_t p = p_begin; p < p_end; ++p) {
-        const int64_t row = p * RPW + lrow;
-        Acc<NC> acc;
+    if (wave >= npass) return;  // whole wave: no barrier follows
+
+    // Wave passes are interleaved over the matrix (pass wave, wave + nwaves, ...), so at any moment the
+    // resident waves read one contiguous stretch of rows: HBM streams best that way. The lane walks
+    // items (pass p, j): row p*RPW + lrow, super-block gb + j*G, j < BPL; the next item's loads are
+    // issued before the current item is computed.
+    const int BPL = (nb + G - 1) / G;
+    const int64_t pass_stride = nwaves * RPW * a.row_stride;
+    constexpr int BYTES = FmtInfo<F>::bytes;
+    int64_t p = wave, row = wave * RPW + lrow;
+    int j = 0;
+    const uint8_t *rowp = w + row * a.row_stride;
+    // Loads are unconditional so the compiler can leave the next item's loads in flight: an item past
+    // the rows or blocks reads block 0 of the matrix instead and is masked by its valid flag.
+    Item<F> cur, nxt;
+    cur.valid = row < a.nrows && gb < nb;
+    cur.load(cur.valid ? rowp + gb * BYTES : w, u);
+    Acc<NC> acc;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
-        if (row < a.nrows) {
-            const uint8_t *wrow = w + row * a.row_stride;
-            for (int b = gb; b < nb; b += G) {
-                const uint8_t *blk = wrow + (int64_t)b * FmtInfo<F>::bytes;
-                if (F == FMT_Q4K)
-                    block_q4K<NC>(blk, u, b, nb, lds_qs, lds_bs, lds_d, acc);
-                else
-                    block_q6K<NC>(blk, u, b, nb, lds_qs, lds_bs, lds_d, acc);
+    for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
+    for (;;) {
+        int jn = j + 1;
+        int64_t pn = p, rown = row;
+        const uint8_t *rowpn = rowp;
+        if (jn == BPL) jn = 0, pn = p + nwaves, rown = row + nwaves * RPW, rowpn = rowp + pass_stride;
+        const bool more = pn < npass;  // uniform over the wave
+        const int bn = gb + jn * G;
+        nxt.valid = more && rown < a.nrows && bn < nb;
+        nxt.load(nxt.valid ? rowpn + bn * BYTES : w, u);
+        const int b = min(gb + j * G, nb - 1);  // LDS column block; an invalid item has zero scales
+        compute_item<NC>(cur, u, b, nb, lds_qs, lds_bs, lds_d, acc);
+        if (j == BPL - 1) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
+            if (row < a.nrows) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    if (lir == c && c < a.ncols) dst[c * a.d_s1 + row] = acc.v[c];
             }
-        }
 #pragma unroll
-        for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
-        if (row < a.nrows) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                if (lir == c && c < a.ncols) dst[c * a.d_s1 + row] = acc.v[c];
+            for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
         }
+        if (!more) break;
+        cur = nxt, j = jn, p = pn, row = rown, rowp = rowpn;
     }
 }
 
@@ -214,16 +262,15 @@ static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
     else lpr = 64;
     const int rpw = 64 / lpr;
     const int64_t npass = (a.nrows + rpw - 1) / rpw;
-    const int64_t target_waves = (int64_t)device_cu_count() * 16;
-    const int ppw = (int)std::max<int64_t>(1, (npass + target_waves - 1) / target_waves);
-    const int64_t waves = (npass + ppw - 1) / ppw;
+    // every wave resident at once: 8 waves per SIMD (the kernels stay within 64 VGPRs)
+    const int64_t waves = std::min<int64_t>(npass, (int64_t)device_cu_count() * 32);
     const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
     const size_t lds = (size_t)NC * a.nb * (256 + ACT_BS_BYTES + 4);
     switch (lpr) {
-    case 8: k_gemv<F, NC, 8><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
-    case 16: k_gemv<F, NC, 16><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
-    case 32: k_gemv<F, NC, 32><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
-    default: k_gemv<F, NC, 64><<<g2, GEMV_WAVES * 64, lds, stream>>>(a, ppw); break;
+    case 8: k_gemv<F, NC, 8><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
+    case 16: k_gemv<F, NC, 16><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
+    case 32: k_gemv<F, NC, 32><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
+    default: k_gemv<F, NC, 64><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
     }
     return hipGetLastError();
 }
