@@ -104,9 +104,17 @@ static int check_weight_layout(const tq_tensor *a, const char *name) {
     if (a->ne[0] % QK) return fail(TQ_STATUS_FAILED, "%s ne[0] = %lld is not a multiple of 256", name, (long long)a->ne[0]);
     if (a->nb[0] != type_size(a->type)) return fail(TQ_STATUS_FAILED, "%s nb[0] is not the block size", name);
     if (a->nb[1] < row_size(a->type, a->ne[0])) return fail(TQ_STATUS_FAILED, "%s rows overlap (nb[1])", name);
-    const size_t align = a->type == TQ_TYPE_Q4_K ? 16 : 2;
-    if ((uintptr_t)a->data % align || a->nb[1] % align || a->nb[2] % align || a->nb[3] % align)
-        return fail(TQ_STATUS_FAILED, "%s data and strides must be %zu-byte aligned", name, align);
+    // Q4_K rows are read as 16-byte words; Q6_K blocks (210 bytes) through the aligned dwords that hold
+    // them, which needs 4-byte aligned matrices and even row strides.
+    const size_t align = a->type == TQ_TYPE_Q4_K ? 16 : 4, row_align = a->type == TQ_TYPE_Q4_K ? 16 : 2;
+    if ((uintptr_t)a->data % align || a->nb[1] % row_align || (a->ne[2] > 1 && a->nb[2] % align) ||
+        (a->ne[3] > 1 && a->nb[3] % align))
+        return fail(TQ_STATUS_FAILED, "%s data, row stride and matrix strides must be %zu, %zu, %zu-byte aligned", name,
+                    align, row_align, align);
+    // the kernels address one matrix with 32-bit byte offsets
+    if ((uint64_t)a->nb[1] * (uint64_t)a->ne[1] >= (1ull << 32) - (1ull << 20))
+        return fail(TQ_STATUS_FAILED, "%s: one matrix of %llu bytes is above the 4 GiB the kernels address", name,
+                    (unsigned long long)((uint64_t)a->nb[1] * (uint64_t)a->ne[1]));
     return TQ_STATUS_SUCCESS;
 }
 

@@ -45,6 +45,13 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
 
 __device__ __forceinline__ int sext8(uint32_t v, int bit) { return (int)(v << (24 - bit)) >> 24; }
 
+// v_bfi_b32: (a & mask) | (b & ~mask) in one instruction (the compiler splits the expression in two).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+    return r;
+}
+
 // Sum over aligned groups of W lanes (W a power of two <= 64), every lane of a group ends with the
 // group's total. Within 16-lane rows the exchanges are DPP moves (quad_perm, row_half_mirror,
 // row_mirror); across rows gfx950's v_permlane16_swap / v_permlane32_swap; no LDS traffic.

@@ -80,9 +80,9 @@ template <int F> struct Item;
 template <> struct Item<FMT_Q4K> {
     uint4 hdr, qv;
     bool valid;
-    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, int u) {
-        hdr = *(const uint4 *)blk;
-        qv = *(const uint4 *)(blk + 16 + 16 * u);
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ w, uint32_t off, int u) {
+        hdr = *(const uint4 *)(w + off);
+        qv = *(const uint4 *)(w + (off + 16 + 16 * u));
     }
 };
 
@@ -93,14 +93,15 @@ template <> struct Item<FMT_Q4K> {
 template <> struct Item<FMT_Q6K> {
     uint32_t a0, a1, a2, b0, b1, b2, h0, h1, h2, t0, t1, t2, t3, t4, sh;
     bool valid;
-    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, int u) {
-        const int h = u >> 2, v = u & 3;
-        sh = (uint32_t)((uintptr_t)blk & 3u);
-        const uint8_t *blk0 = blk - sh;  // 4-byte aligned
-        const uint32_t *pa = (const uint32_t *)(blk0 + 64 * h + 8 * v);
-        const uint32_t *pb = (const uint32_t *)(blk0 + 64 * h + 32 + 8 * v);
-        const uint32_t *ph = (const uint32_t *)(blk0 + 128 + 32 * h + 8 * v);
-        const uint32_t *pt = (const uint32_t *)(blk0 + 192);
+    // w is 4-byte aligned (checked by the host); off is the block's byte offset, even.
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ w, uint32_t off, int u) {
+        const uint32_t h = (uint32_t)u >> 2, v = (uint32_t)u & 3;
+        sh = off & 3u;
+        const uint32_t o0 = off - sh;  // 4-byte aligned
+        const uint32_t *pa = (const uint32_t *)(w + (o0 + 64 * h + 8 * v));
+        const uint32_t *pb = (const uint32_t *)(w + (o0 + 64 * h + 32 + 8 * v));
+        const uint32_t *ph = (const uint32_t *)(w + (o0 + 128 + 32 * h + 8 * v));
+        const uint32_t *pt = (const uint32_t *)(w + (o0 + 192));
         a0 = pa[0], a1 = pa[1], a2 = pa[2];
         b0 = pb[0], b1 = pb[1], b2 = pb[2];
         h0 = ph[0], h1 = ph[1], h2 = ph[2];
@@ -159,11 +160,16 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
     const float d = it.valid ? half_bits_to_float(it.t4 >> (8 * sh)) : 0.f;
     const int pos = 8 * (v >> 1);
     const int sc0 = sext8(s01, pos), sc1 = sext8(s01, pos + 16), sc2 = sext8(s23, pos), sc3 = sext8(s23, pos + 16);
+    // 6-bit codes: low nibble from ql, bits 4-5 from the qh field of the quarter. Hl keeps qh bits
+    // (0,1) and (4,5) of every byte, Hh bits (2,3) and (6,7) moved down by two; a bit-field insert then
+    // merges nibble and high bits without the neighbour byte's bits leaking in.
     const uint32_t m4 = 0x0f0f0f0fu;
-    const uint32_t q00 = (A0 & m4) | ((H0 & 0x03030303u) << 4), q01 = (A1 & m4) | ((H1 & 0x03030303u) << 4);
-    const uint32_t q10 = (B0 & m4) | ((H0 & 0x0c0c0c0cu) << 2), q11 = (B1 & m4) | ((H1 & 0x0c0c0c0cu) << 2);
-    const uint32_t q20 = ((A0 >> 4) & m4) | (H0 & 0x30303030u), q21 = ((A1 >> 4) & m4) | (H1 & 0x30303030u);
-    const uint32_t q30 = ((B0 >> 4) & m4) | ((H0 >> 2) & 0x30303030u), q31 = ((B1 >> 4) & m4) | ((H1 >> 2) & 0x30303030u);
+    const uint32_t Hl0 = H0 & 0x33333333u, Hl1 = H1 & 0x33333333u;
+    const uint32_t Hh0 = (H0 >> 2) & 0x33333333u, Hh1 = (H1 >> 2) & 0x33333333u;
+    const uint32_t q00 = bfi(m4, A0, Hl0 << 4), q01 = bfi(m4, A1, Hl1 << 4);
+    const uint32_t q10 = bfi(m4, B0, Hh0 << 4), q11 = bfi(m4, B1, Hh1 << 4);
+    const uint32_t q20 = bfi(m4, A0 >> 4, Hl0), q21 = bfi(m4, A1 >> 4, Hl1);
+    const uint32_t q30 = bfi(m4, B0 >> 4, Hh0), q31 = bfi(m4, B1 >> 4, Hh1);
     // the -32 offset enters once per 16-element group, on the even lane of the pair sharing it
     const int even = (v & 1) ? 0 : -32;
 #pragma unroll
@@ -210,60 +216,73 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
 
     // Wave passes are interleaved over the matrix (pass wave, wave + nwaves, ...), so at any moment the
     // resident waves read one contiguous stretch of rows: HBM streams best that way. The lane walks
-    // items (pass p, j): row p*RPW + lrow, super-block gb + j*G, j < BPL; the next item's loads are
-    // issued before the current item is computed.
+    // items (pass p, j): row p*RPW + lrow, super-block gb + j*G, j < BPL. The next item's loads are
+    // issued before the current item is computed; the two item registers alternate (the loop body
+    // is unrolled twice) so nothing is copied. Weights are addressed by 32-bit byte offsets from the
+    // matrix base (the host keeps each matrix below 4 GiB).
     const int BPL = (nb + G - 1) / G;
-    const int64_t pass_stride = nwaves * RPW * a.row_stride;
+    const int nrows = (int)a.nrows;
+    const uint32_t row_stride = (uint32_t)a.row_stride;
     constexpr int BYTES = FmtInfo<F>::bytes;
-    int64_t p = wave, row = wave * RPW + lrow;
-    int j = 0;
-    const uint8_t *rowp = w + row * a.row_stride;
+    struct Pos {
+        int p, j, row;
+        uint32_t row_off;
+    };
+    Pos cur{(int)wave, 0, (int)wave * RPW + lrow, 0};
+    cur.row_off = (uint32_t)cur.row * row_stride;
+    const int nw = (int)nwaves;
+    const uint32_t pass_stride = (uint32_t)(nw * RPW) * row_stride;
     // Loads are unconditional so the compiler can leave the next item's loads in flight: an item past
     // the rows or blocks reads block 0 of the matrix instead and is masked by its valid flag.
-    Item<F> cur, nxt;
-    cur.valid = row < a.nrows && gb < nb;
-    cur.load(cur.valid ? rowp + gb * BYTES : w, u);
+    auto load = [&](Item<F> &it, const Pos &q) {
+        const int b = gb + q.j * G;
+        it.valid = q.row < nrows && b < nb;
+        it.load(w, it.valid ? q.row_off + (uint32_t)(b * BYTES) : 0u, u);
+    };
     Acc<NC> acc;
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
-    for (;;) {
-        int jn = j + 1;
-        int64_t pn = p, rown = row;
-        const uint8_t *rowpn = rowp;
-        if (jn == BPL) jn = 0, pn = p + nwaves, rown = row + nwaves * RPW, rowpn = rowp + pass_stride;
-        const bool more = pn < npass;  // uniform over the wave
-        const int bn = gb + jn * G;
-        nxt.valid = more && rown < a.nrows && bn < nb;
-        nxt.load(nxt.valid ? rowpn + bn * BYTES : w, u);
-        const int b = min(gb + j * G, nb - 1);  // LDS column block; an invalid item has zero scales
-        compute_item<NC>(cur, u, b, nb, lds_qs, lds_bs, lds_d, acc);
-        if (j == BPL - 1) {
+    // One step: issue the next item's loads into `nxt`, compute `now`, finish the row if it ends here.
+    auto step = [&](Item<F> &now, Item<F> &nxt) -> bool {
+        Pos n = cur;
+        if (++n.j == BPL) n.j = 0, n.p += nw, n.row += nw * RPW, n.row_off += pass_stride;
+        const bool more = n.p < (int)npass;  // uniform over the wave
+        load(nxt, n);
+        const int b = min(gb + cur.j * G, nb - 1);  // LDS column block; an invalid item has zero scales
+        compute_item<NC>(now, u, b, nb, lds_qs, lds_bs, lds_d, acc);
+        if (cur.j == BPL - 1) {
 #pragma unroll
             for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
-            if (row < a.nrows) {
+            if (cur.row < nrows) {
 #pragma unroll
                 for (int c = 0; c < NC; ++c)
-                    if (lir == c && c < a.ncols) dst[c * a.d_s1 + row] = acc.v[c];
+                    if (lir == c && c < a.ncols) dst[c * a.d_s1 + cur.row] = acc.v[c];
             }
 #pragma unroll
             for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
         }
-        if (!more) break;
-        cur = nxt, j = jn, p = pn, row = rown, rowp = rowpn;
+        cur = n;
+        return more;
+    };
+    Item<F> A, B;
+    load(A, cur);
+    for (;;) {
+        if (!step(A, B)) break;
+        if (!step(B, A)) break;
     }
 }
 
 template <int F, int NC>
 static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
-    int lpr;
-    if (a.nb <= 1) lpr = 8;
-    else if (a.nb <= 2) lpr = 16;
-    else if (a.nb <= 4) lpr = 32;
-    else lpr = 64;
+    // Lanes per row: fewer lanes per row amortize the cross-lane row sum over more super-blocks, as long
+    // as there are enough row passes to keep every wave slot of the GPU busy (8 waves per SIMD).
+    const int64_t slots = (int64_t)device_cu_count() * 32;
+    int lpr = 8, lpr_max = 8;
+    while (lpr_max < 64 && lpr_max < 8 * a.nb) lpr_max *= 2;  // no more super-block groups than blocks
+    while (lpr < lpr_max && (lpr < 8 * std::min(a.nb, 2) || (a.nrows + 64 / lpr - 1) / (64 / lpr) < slots)) lpr *= 2;
     const int rpw = 64 / lpr;
     const int64_t npass = (a.nrows + rpw - 1) / rpw;
-    // every wave resident at once: 8 waves per SIMD (the kernels stay within 64 VGPRs)
-    const int64_t waves = std::min<int64_t>(npass, (int64_t)device_cu_count() * 32);
+    const int64_t waves = std::min<int64_t>(npass, slots);
     const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
     const size_t lds = (size_t)NC * a.nb * (256 + ACT_BS_BYTES + 4);
     switch (lpr) {
