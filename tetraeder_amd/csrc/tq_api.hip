@@ -229,15 +229,73 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     return TQ_STATUS_SUCCESS;
 }
 
+static int check_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, const tq_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(as, "as")) || (rc = check_tensor(b, "b")) || (rc = check_tensor(ids, "ids")) ||
+        (rc = check_tensor(dst, "dst")))
+        return rc;
+    if ((rc = check_weight_layout(as, "as")) || (rc = check_f32(b, "b")) || (rc = check_f32(dst, "dst"))) return rc;
+    if (ids->type != TQ_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4 || (uintptr_t)ids->data % 4)
+        return fail(TQ_STATUS_FAILED, "ids must be I32 with 4-byte elements");
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = b->ne[1];
+    if (as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "MUL_MAT_ID takes 3-d experts and b, 2-d ids");
+    if (b->ne[0] != as->ne[0]) return fail(TQ_STATUS_FAILED, "as ne[0] %lld != b ne[0] %lld", (long long)as->ne[0], (long long)b->ne[0]);
+    if (b->ne[2] != T) return fail(TQ_STATUS_FAILED, "b ne[2] %lld != ids ne[1] %lld", (long long)b->ne[2], (long long)T);
+    if (ne11 < 1 || n_used % ne11) return fail(TQ_STATUS_FAILED, "ids ne[0] %lld is not a multiple of b ne[1] %lld", (long long)n_used, (long long)ne11);
+    if (dst->ne[0] != as->ne[1] || dst->ne[1] != n_used || dst->ne[2] != T || dst->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "dst shape is not [as.ne1, ids.ne0, ids.ne1]");
+    if (as->ne[2] < 1 || as->ne[2] > 65535 || n_used * T >= (1ll << 31))
+        return fail(TQ_STATUS_FAILED, "expert or slot count out of range");
+    const int nb = (int)(as->ne[0] / QK);
+    if ((size_t)8 * nb * gemv_lds_per_col_block() + 64 > gemv_max_lds())
+        return fail(TQ_STATUS_FAILED, "K = %lld is above the MUL_MAT_ID limit", (long long)as->ne[0]);
+    return TQ_STATUS_SUCCESS;
+}
+
+static size_t mmid_workspace(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids) {
+    return q8_bytes(b) + align_up(mmid_route_bytes((int)as->ne[2], ids->ne[0] * ids->ne[1]), 256);
+}
+
 size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids) {
-    (void)as, (void)b, (void)ids;
-    return 0;
+    if (!as || !b || !ids) return 0;
+    return mmid_workspace(as, b, ids);
 }
 
 int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
                   size_t workspace_size, void *stream) {
-    (void)as, (void)b, (void)ids, (void)dst, (void)workspace, (void)workspace_size, (void)stream;
-    return fail(TQ_STATUS_FAILED, "MUL_MAT_ID is not built yet");
+    int rc;
+    if ((rc = check_mul_mat_id(as, b, ids, dst))) return rc;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    if (n_used * T == 0 || as->ne[1] == 0) return TQ_STATUS_SUCCESS;
+    const size_t need = mmid_workspace(as, b, ids);
+    if (workspace && workspace_size < need)
+        return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
+    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+    if (!ws) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], 1, b->nb[1], b->nb[2], b->nb[3], ws, s),
+                        "quantize_q8_K launch")))
+        return rc;
+    MmidArgs m{};
+    m.w = (const uint8_t *)as->data;
+    m.w_s1 = (int64_t)as->nb[1];
+    m.w_s2 = (int64_t)as->nb[2];
+    m.nrows = (int32_t)as->ne[1];
+    m.nb = (int32_t)(as->ne[0] / QK);
+    m.n_expert = (int32_t)as->ne[2];
+    m.n_used = (int32_t)n_used;
+    m.ntok = (int32_t)T;
+    m.ne11 = (int32_t)b->ne[1];
+    m.ids = (const uint8_t *)ids->data;
+    m.ids_s0 = (int64_t)ids->nb[0];
+    m.ids_s1 = (int64_t)ids->nb[1];
+    m.q8 = ws;
+    m.dst = (float *)dst->data;
+    m.d_s1 = (int64_t)(dst->nb[1] / 4);
+    m.d_s2 = (int64_t)(dst->nb[2] / 4);
+    m.route = (int32_t *)(ws + q8_bytes(b));
+    return check_hip(launch_mul_mat_id(as->type, m, s), "mul_mat_id launch");
 }
 
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {

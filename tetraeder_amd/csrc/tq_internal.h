@@ -38,6 +38,25 @@ hipError_t launch_gemv(int type, const GemvArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }
 
+// Lanes per weight row for an nrows x (nb super-blocks) matrix when `slots` waves can be resident.
+int gemv_lanes_per_row(int nb, int64_t nrows, int64_t slots);
+
+// MUL_MAT_ID over Q8_K activations: routing on the device, then one expert GEMV per routed expert.
+struct MmidArgs {
+    const uint8_t *w;        // stacked experts [K, N, n_expert]
+    int64_t w_s1, w_s2;      // bytes between rows / experts
+    int32_t nrows, nb;       // N, K/256
+    int32_t n_expert, n_used, ntok, ne11;
+    const uint8_t *ids;      // I32 [n_used, T]
+    int64_t ids_s0, ids_s1;  // bytes
+    const uint8_t *q8;       // Q8_K rows: activation row (j % ne11) of token t is row t*ne11 + j % ne11
+    float *dst;              // [N, n_used, T]
+    int64_t d_s1, d_s2;      // floats
+    int32_t *route;          // workspace: routing lists (mmid_route_bytes)
+};
+size_t mmid_route_bytes(int n_expert, int64_t n_slots);
+hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream);
+
 // Device properties cached per device.
 int device_cu_count();
 
