@@ -207,7 +207,10 @@ def main():
     torch.cuda.empty_cache()
 
     secondary = {}
+    moe = {}
     if not args.no_secondary:
+        moe = bench_moe(ggml, torch, np, dev)
+        secondary["moe_step"] = moe
         secondary.update(bench_secondary(ggml, torch, dev))
 
     line = {
@@ -221,9 +224,59 @@ def main():
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv<q6_K,1 col>", "kernel_us": round(kern_us, 2)},
         "cpu_baseline": cpu,
+        "moe_mul_mat_id_us_per_token": {t: v["us_per_token"] for t, v in moe.items()},
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
+
+
+MOE_EXPERT_BYTES = 2 * 884736 + 1290240  # gate + up Q4_K [2048 x 768] + down Q6_K [768 x 2048]
+
+
+def moe_ids(np, tokens, seed, n_expert=128, used=8, neg_frac=0.1):
+    """top-8 of softmax over N(0,1) router logits, then neg_frac of the id slots set to -1."""
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((tokens, n_expert)).astype(np.float32)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :used].astype(np.int32)
+    ids[rng.random(ids.shape) < neg_frac] = -1
+    return ids
+
+
+def bench_moe(ggml, torch, np, dev, layers=4, routings=8):
+    """The MoE expert FFN step (gate, up, swiglu, down) at Qwen3-30B-A3B shapes: 128 experts, n_embd
+    2048, n_ff 768, gate/up Q4_K, down Q6_K, top-8 with 10% -1. Steps rotate over `layers` weight copies
+    (4 x 392 MB) and `routings` seeded id sets, captured in a HIP graph; the roofline bytes are the
+    unique valid experts of each step's ids."""
+    n_embd, n_ff, E = 2048, 768, 128
+    L = []
+    for l in range(layers):
+        L.append(tuple(make_weights(ggml, torch, ty, k, n * E, 1, seed=100 + 3 * l + i, dev=dev)[0]
+                       for i, (ty, k, n) in enumerate(((ggml.Type.Q4_K, n_embd, n_ff), (ggml.Type.Q4_K, n_embd, n_ff),
+                                                       (ggml.Type.Q6_K, n_ff, n_embd)))))
+    L = [tuple(ggml.QTensor(w.type, (w.ne[0], w.ne[1] // E, E), w.data) for w in lw) for lw in L]
+    res = {}
+    for T in (1, 2, 4, 8, 16):
+        ids_np = [moe_ids(np, T, seed=1000 * T + r) for r in range(routings)]
+        uniq = [len(set(int(e) for e in x.reshape(-1) if e >= 0)) for x in ids_np]
+        ids = [torch.from_numpy(x).to(dev) for x in ids_np]
+        x = torch.randn((T, 1, n_embd), device=dev)
+        out = torch.empty((T, 8, n_embd), device=dev)
+        ws = torch.empty(max(1, ggml.moe_ffn_workspace_size(L[0][0], x, ids[0])), dtype=torch.uint8, device=dev)
+        n = layers * routings
+        step = lambda i: ggml.moe_ffn(*L[i % layers], x, ids[(i // layers) % routings], out=out, workspace=ws)  # noqa
+        us = time_graph(torch, step, n)
+        mean_bytes = sum(uniq[(i // layers) % routings] for i in range(n)) / n * MOE_EXPERT_BYTES
+        gbs = mean_bytes / us / 1e3
+        res[str(T)] = {"us_per_step": round(us, 2), "us_per_token": round(us / T, 2),
+                       "unique_experts": round(mean_bytes / MOE_EXPERT_BYTES, 2),
+                       "weight_MB": round(mean_bytes / 1e6, 2), "GBps": round(gbs, 1),
+                       "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"moe T={T}: {res[str(T)]}")
+    del L
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_secondary(ggml, torch, dev):

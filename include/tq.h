@@ -110,6 +110,24 @@ size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, con
 int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
                   size_t workspace_size, void *stream);
 
+/* Workspace bytes tq_moe_ffn needs for these operands. */
+size_t tq_moe_ffn_workspace_size(const tq_tensor *gate_exps, const tq_tensor *b, const tq_tensor *ids);
+
+/* The MoE expert FFN of one layer, the node sequence of weighted_experts
+ * (crates/model/src/qwen3moe.rs:2899-2914):
+ *   up = MUL_MAT_ID(up_exps, b, ids); gate = MUL_MAT_ID(gate_exps, b, ids);
+ *   act = swiglu_split(gate, up) = silu(gate) * up; dst = MUL_MAT_ID(down_exps, act, ids) * weights
+ * with gate_exps/up_exps [n_embd, n_ff, n_expert], down_exps [n_ff, n_embd, n_expert] (Q4_K or Q6_K
+ * each), b F32 [n_embd, 1, T], ids I32 [n_used, T], weights F32 [1, n_used, T] or NULL (no scaling),
+ * dst F32 [n_embd, n_used, T]. Slots with id < 0 read no weights and get exact zero rows. act is
+ * quantized to Q8_K as the down MUL_MAT_ID would. Up to 256 slots (n_used * T) the whole step is two
+ * launches (gate and up together; then swiglu, the Q8_K pass and down fused in one kernel); above that
+ * the nodes run as separate MUL_MAT_ID launches with device routing. The sum over slots (sum_experts,
+ * qwen3moe.rs:2917-2923) stays with the caller. */
+int tq_moe_ffn(const tq_tensor *gate_exps, const tq_tensor *up_exps, const tq_tensor *down_exps, const tq_tensor *b,
+               const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
+               void *stream);
+
 /* Dequantize n elements of type (Q4_K, Q6_K or Q8_K; n a multiple of 256) from src to F32 dst.
  * Replaces ggml_get_type_traits(ty)->to_float as used by quant::to_f32
  * (crates/ggml-sys/src/ggml/quant.rs:20-48) for device buffers. */

@@ -101,11 +101,16 @@ def test_gemv_golden(gpu, tname):
 
 
 def test_workspace_argument(gpu):
+    """Decode-size activations are quantized inside the GEMV workgroups and need no workspace; larger
+    ones need the reported size and a smaller workspace is rejected."""
     _case("workspace")
     ty = ggml.Type.Q4_K
     w = make_weights(ty, 1024, 64, 1, seed=7, device=gpu)
-    x = torch.from_numpy(normal((3, 1024), 8)).to(gpu)
+    small = torch.from_numpy(normal((2, 1024), 8)).to(gpu)
+    assert ggml.mul_mat_workspace_size(w, small) == 0
+    x = torch.from_numpy(normal((20, 1024), 9)).to(gpu)
     need = ggml.mul_mat_workspace_size(w, x)
+    assert need >= 20 * 4 * 292
     ws = torch.empty(need, dtype=torch.uint8, device=gpu)
     a = ggml.mul_mat(w, x, workspace=ws)
     b = ggml.mul_mat(w, x)

@@ -128,6 +128,10 @@ static int check_f32(const tq_tensor *t, const char *name) {
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Decode-size activations (at most two Q8_K blocks per wave of a GEMV workgroup) are quantized by each
+// workgroup into LDS: one launch instead of two. Larger ones get a quantization pass of their own.
+static bool quantize_in_workgroup(int64_t ncols, int nb) { return ncols * nb <= 16; }
+
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
 
 }  // namespace tq
@@ -159,8 +163,8 @@ int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream) {
 }
 
 size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b) {
-    (void)a;
-    return b && b->type == TQ_TYPE_F32 ? q8_bytes(b) : 0;
+    if (!a || !b || b->type != TQ_TYPE_F32 || quantize_in_workgroup(b->ne[1], (int)(a->ne[0] / QK))) return 0;
+    return q8_bytes(b);
 }
 
 int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
@@ -193,7 +197,10 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
 
     hipStream_t s = (hipStream_t)stream;
     void *q8 = b->data;
-    if (!pre_quantized) {
+    // Small activations (decode) are quantized inside each GEMV workgroup, straight into LDS: one launch
+    // instead of two. Larger ones get their own quantization pass first.
+    const bool in_wg = !pre_quantized && quantize_in_workgroup(b->ne[1], nb);
+    if (!pre_quantized && !in_wg) {
         const size_t need = q8_bytes(b);
         if (workspace && workspace_size < need)
             return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
@@ -221,6 +228,13 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     g.d_s1 = (int64_t)(dst->nb[1] / 4);
     g.d_s2 = (int64_t)(dst->nb[2] / 4);
     g.d_s3 = (int64_t)(dst->nb[3] / 4);
+    if (in_wg) {
+        g.b = (const float *)b->data;
+        g.b_s1 = (int64_t)(b->nb[1] / 4);
+        g.b_s2 = (int64_t)(b->nb[2] / 4);
+        g.b_s3 = (int64_t)(b->nb[3] / 4);
+        g.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0 && b->nb[3] % 16 == 0;
+    }
     for (int64_t c0 = 0; c0 < b->ne[1]; c0 += nc_max) {
         g.col0 = (int32_t)c0;
         g.ncols = (int32_t)std::min<int64_t>(nc_max, b->ne[1] - c0);
@@ -274,9 +288,6 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
     if (!ws) return rc;
     hipStream_t s = (hipStream_t)stream;
-    if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], 1, b->nb[1], b->nb[2], b->nb[3], ws, s),
-                        "quantize_q8_K launch")))
-        return rc;
     MmidArgs m{};
     m.w = (const uint8_t *)as->data;
     m.w_s1 = (int64_t)as->nb[1];
@@ -295,7 +306,116 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     m.d_s1 = (int64_t)(dst->nb[1] / 4);
     m.d_s2 = (int64_t)(dst->nb[2] / 4);
     m.route = (int32_t *)(ws + q8_bytes(b));
+    if (n_used * T <= mmid_small_max_slots()) {
+        // decode: one launch, routing resolved per workgroup, activations quantized in LDS
+        const int b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0;
+        return check_hip(launch_mul_mat_id_small(as->type, m, (const float *)b->data, (int64_t)(b->nb[1] / 4),
+                                                 (int64_t)(b->nb[2] / 4), b_vec, s),
+                         "mul_mat_id launch");
+    }
+    if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], 1, b->nb[1], b->nb[2], b->nb[3], ws, s),
+                        "quantize_q8_K launch")))
+        return rc;
     return check_hip(launch_mul_mat_id(as->type, m, s), "mul_mat_id launch");
+}
+
+static int check_moe(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
+                     const tq_tensor *ids, const tq_tensor *w, const tq_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(gate, "gate")) || (rc = check_tensor(up, "up")) || (rc = check_tensor(down, "down"))) return rc;
+    if ((rc = check_weight_layout(gate, "gate")) || (rc = check_weight_layout(up, "up")) ||
+        (rc = check_weight_layout(down, "down")))
+        return rc;
+    const int64_t n_embd = gate->ne[0], n_ff = gate->ne[1], E = gate->ne[2];
+    if (up->ne[0] != n_embd || up->ne[1] != n_ff || up->ne[2] != E || down->ne[0] != n_ff || down->ne[1] != n_embd ||
+        down->ne[2] != E)
+        return fail(TQ_STATUS_FAILED, "gate/up must be [n_embd, n_ff, n_expert] and down [n_ff, n_embd, n_expert]");
+    if (n_ff % QK) return fail(TQ_STATUS_FAILED, "n_ff = %lld is not a multiple of 256", (long long)n_ff);
+    if (b->ne[1] != 1) return fail(TQ_STATUS_FAILED, "b must be [n_embd, 1, T] (one activation row per token)");
+    tq_tensor act = *dst;
+    act.ne[0] = n_ff;  // shape check of the down MUL_MAT_ID input
+    if ((rc = check_mul_mat_id(gate, b, ids, &act))) return rc;
+    if (dst->ne[0] != n_embd || dst->ne[1] != ids->ne[0] || dst->ne[2] != ids->ne[1] || dst->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "dst shape is not [n_embd, n_used, T]");
+    if ((rc = check_f32(dst, "dst"))) return rc;
+    if (w) {
+        if ((rc = check_tensor(w, "weights")) || (rc = check_f32(w, "weights"))) return rc;
+        if (w->ne[0] != 1 || w->ne[1] != ids->ne[0] || w->ne[2] != ids->ne[1])
+            return fail(TQ_STATUS_FAILED, "router weights must be [1, n_used, T]");
+    }
+    if ((size_t)8 * (n_ff / QK) * gemv_lds_per_col_block() + 64 > gemv_max_lds())
+        return fail(TQ_STATUS_FAILED, "n_ff = %lld is above the limit", (long long)n_ff);
+    return TQ_STATUS_SUCCESS;
+}
+
+static size_t moe_workspace(const tq_tensor *gate, const tq_tensor *b, const tq_tensor *ids) {
+    const int64_t n_slots = ids->ne[0] * ids->ne[1], n_ff = gate->ne[1];
+    size_t bytes = align_up((size_t)3 * n_slots * n_ff * 4, 256);  // gate, up (and act when composed)
+    if (n_slots > mmid_small_max_slots()) {
+        tq_tensor a = *b;
+        a.ne[0] = n_ff, a.ne[1] = ids->ne[0];
+        bytes += std::max(mmid_workspace(gate, b, ids), q8_bytes(&a) + align_up(mmid_route_bytes((int)gate->ne[2], n_slots), 256));
+    }
+    return bytes;
+}
+
+size_t tq_moe_ffn_workspace_size(const tq_tensor *gate, const tq_tensor *b, const tq_tensor *ids) {
+    if (!gate || !b || !ids) return 0;
+    return moe_workspace(gate, b, ids);
+}
+
+int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
+               const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
+               void *stream) {
+    int rc;
+    if (!gate || !up || !down || !b || !ids || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor");
+    if ((rc = check_moe(gate, up, down, b, ids, weights, dst))) return rc;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], n_slots = n_used * T;
+    const int64_t n_embd = gate->ne[0], n_ff = gate->ne[1];
+    if (n_slots == 0) return TQ_STATUS_SUCCESS;
+    const size_t need = moe_workspace(gate, b, ids);
+    if (workspace && workspace_size < need)
+        return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
+    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+    if (!ws) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    float *gu = (float *)ws;
+    if (n_slots <= mmid_small_max_slots()) {
+        MoeArgs m{};
+        m.gate = (const uint8_t *)gate->data, m.up = (const uint8_t *)up->data, m.down = (const uint8_t *)down->data;
+        m.g_s1 = (int64_t)gate->nb[1], m.g_s2 = (int64_t)gate->nb[2];
+        m.u_s1 = (int64_t)up->nb[1], m.u_s2 = (int64_t)up->nb[2];
+        m.dn_s1 = (int64_t)down->nb[1], m.dn_s2 = (int64_t)down->nb[2];
+        m.n_embd = (int32_t)n_embd, m.n_ff = (int32_t)n_ff, m.n_expert = (int32_t)gate->ne[2];
+        m.n_used = (int32_t)n_used, m.ntok = (int32_t)T;
+        m.ids = (const uint8_t *)ids->data, m.ids_s0 = (int64_t)ids->nb[0], m.ids_s1 = (int64_t)ids->nb[1];
+        m.b = (const float *)b->data, m.b_s2 = (int64_t)(b->nb[2] / 4);
+        m.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[2] % 16 == 0;
+        if (weights) m.rw = (const float *)weights->data, m.rw_s1 = (int64_t)(weights->nb[1] / 4),
+                     m.rw_s2 = (int64_t)(weights->nb[2] / 4);
+        m.gu = gu;
+        m.dst = (float *)dst->data, m.o_s1 = (int64_t)(dst->nb[1] / 4), m.o_s2 = (int64_t)(dst->nb[2] / 4);
+        return check_hip(launch_moe_ffn(gate->type, up->type, down->type, m, s), "moe_ffn launch");
+    }
+    // Many tokens: the same nodes composed, MUL_MAT_ID with device routing and elementwise glue.
+    uint8_t *rest = ws + align_up((size_t)3 * n_slots * n_ff * 4, 256);
+    const size_t rest_size = need - (size_t)(rest - ws);
+    float *g_out = gu, *u_out = gu + n_slots * n_ff, *act = gu + 2 * n_slots * n_ff;
+    tq_tensor o = *dst;
+    o.ne[0] = n_ff, o.nb[0] = 4, o.nb[1] = (size_t)n_ff * 4, o.nb[2] = (size_t)n_ff * 4 * n_used, o.nb[3] = o.nb[2] * T;
+    o.data = g_out;
+    if ((rc = tq_mul_mat_id(gate, b, ids, &o, rest, rest_size, stream))) return rc;
+    o.data = u_out;
+    if ((rc = tq_mul_mat_id(up, b, ids, &o, rest, rest_size, stream))) return rc;
+    if ((rc = check_hip(launch_swiglu(g_out, u_out, act, n_slots * n_ff, s), "swiglu launch"))) return rc;
+    o.data = act;
+    if ((rc = tq_mul_mat_id(down, &o, ids, dst, rest, rest_size, stream))) return rc;
+    if (weights)
+        return check_hip(launch_scale_rows((float *)dst->data, n_embd, (int)n_used, T, (const float *)weights->data,
+                                           (int64_t)(weights->nb[1] / 4), (int64_t)(weights->nb[2] / 4),
+                                           (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4), s),
+                         "scale_rows launch");
+    return TQ_STATUS_SUCCESS;
 }
 
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {

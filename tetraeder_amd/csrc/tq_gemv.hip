@@ -19,8 +19,15 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
     uint8_t *lds_qs = lds;
     int16_t *lds_bs = (int16_t *)(lds + NC * nb * 256);
     float *lds_d = (float *)(lds + NC * nb * (256 + ACT_BS_BYTES));
-    const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
-    stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
+    if (a.b) {
+        const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;
+        const int64_t b_s1 = a.b_s1;
+        stage_activations_f32<F, NC>([&](int c) { return b + c * b_s1; }, a.b_vec != 0, nb, a.ncols, lds_qs, lds_bs,
+                                     lds_d);
+    } else {
+        const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
+        stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
+    }
     __syncthreads();
 
     const int ncols = a.ncols;

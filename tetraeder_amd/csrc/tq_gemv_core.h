@@ -71,6 +71,84 @@ __device__ __forceinline__ void stage_activations(ColSrc col_src, int nb, int nc
     }
 }
 
+// One wave quantizes 256 floats (lane l holds elements 4l .. 4l+3 in v) to Q8_K straight into the LDS
+// staging layout of format F (the block at column-block cb). Bit-identical to k_quantize_q8_K (ggml's quantize_row_q8_K): first-occurrence
+// argmax of |x|, iscale = -127/max with IEEE division, round-half-even, d = 1/iscale, zero block -> 0.
+template <int F>
+__device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], int cb, uint8_t *lds_qs, int16_t *lds_bs,
+                                                          float *lds_d) {
+    const int lane = lane_id();
+    float amax = 0.f, vmax = 0.f;
+    int imax = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float x = fabsf(v[j]);
+        if (x > amax) amax = x, vmax = v[j], imax = lane * 4 + j;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float a2 = __shfl_xor(amax, off, 64);
+        const float v2 = __shfl_xor(vmax, off, 64);
+        const int i2 = __shfl_xor(imax, off, 64);
+        if (a2 > amax || (a2 == amax && i2 < imax)) amax = a2, vmax = v2, imax = i2;
+    }
+    uint32_t packed = 0;
+    int sum = 0;
+    float d = 0.f;
+    if (amax != 0.f) {
+        const float iscale = __fdiv_rn(-127.f, vmax);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int q = (int)rintf(__fmul_rn(iscale, v[j]));
+            q = q < 127 ? q : 127;
+            sum += q;
+            packed |= (uint32_t)(q & 0xff) << (8 * j);
+        }
+        d = __fdiv_rn(1.f, iscale);
+    }
+    *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * lane)) = packed;
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);  // lanes 4g..4g+3 hold the sum of group g
+    constexpr int SLOTS = F == FMT_Q4K ? 2 : 4;
+    const int slot = lane < 8 * SLOTS ? lane : 0;
+    const int g = act_bs_src<F>(slot / SLOTS, slot % SLOTS);
+    const int bs = __shfl(sum, 4 * g, 64);
+    if (lane < 8 * SLOTS) lds_bs[cb * (ACT_BS_BYTES / 2) + lane] = (int16_t)bs;
+    if (lane == 0) lds_d[cb] = d;
+}
+
+// The same for 256 floats read from src (lane l takes src[4l .. 4l+3]).
+template <int F>
+__device__ __forceinline__ void wave_quantize_to_lds(const float *__restrict__ src, bool vec, int cb, uint8_t *lds_qs,
+                                                     int16_t *lds_bs, float *lds_d) {
+    const int lane = lane_id();
+    float v[4];
+    if (vec) {
+        const float4 f = *(const float4 *)(src + 4 * lane);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = src[4 * lane + j];
+    }
+    wave_quantize_vals_to_lds<F>(v, cb, lds_qs, lds_bs, lds_d);
+}
+
+// Stages NC columns given as F32 rows (column c starts at col_f32(c), nb*256 floats; zeros for c >=
+// ncols), quantizing each 256-float block to Q8_K in LDS with one wave.
+template <int F, int NC, class ColF32>
+__device__ __forceinline__ void stage_activations_f32(ColF32 col_f32, bool vec, int nb, int ncols, uint8_t *lds_qs,
+                                                      int16_t *lds_bs, float *lds_d) {
+    const int wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int i = wid; i < ncols * nb; i += nw) {
+        const int c = i / nb, b = i - c * nb;
+        wave_quantize_to_lds<F>(col_f32(c) + (size_t)b * QK, vec, c * nb + b, lds_qs, lds_bs, lds_d);
+    }
+    // padding columns: zero scales give zero contributions
+    for (int i = ncols * nb + threadIdx.x; i < NC * nb; i += blockDim.x) lds_d[i] = 0.f;
+    for (int i = ncols * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x) ((uint32_t *)lds_qs)[i] = 0;
+    for (int i = ncols * nb * 32 + threadIdx.x; i < NC * nb * 32; i += blockDim.x) lds_bs[i] = 0;
+}
+
 template <int NC> struct Acc {
     float v[NC];
 };

@@ -1,0 +1,45 @@
+// tq_glue.hip -- the elementwise step glue around MUL_MAT_ID in the MoE expert FFN for large token
+// counts (crates/model/src/qwen3moe.rs:2909-2913): act = swiglu_split(gate, up) = silu(gate) * up, and the
+// multiply of expert outputs by the router weights.
+#include "tq_device.h"
+#include "tq_internal.h"
+
+namespace tq {
+
+__global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gate, const float *__restrict__ up,
+                                                float *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = gate[i];
+    out[i] = x / (1.0f + expf(-x)) * up[i];  // ggml_silu_f32(x) * up
+}
+
+// rows of `row_len` floats, row r = j + n_used * t scaled by w[j * w_s1 + t * w_s2]
+__global__ __launch_bounds__(256) void k_scale_rows(float *__restrict__ x, int64_t row_len, int n_used, int64_t nrows,
+                                                    const float *__restrict__ w, int64_t w_s1, int64_t w_s2,
+                                                    int64_t x_s1, int64_t x_s2) {
+    const int64_t r = blockIdx.y;
+    if (r >= nrows) return;
+    const int j = (int)(r % n_used), t = (int)(r / n_used);
+    const float s = w[j * w_s1 + t * w_s2];
+    float *row = x + j * x_s1 + t * x_s2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < row_len; i += (int64_t)gridDim.x * blockDim.x)
+        row[i] *= s;
+}
+
+hipError_t launch_swiglu(const float *gate, const float *up, float *out, int64_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    k_swiglu<<<dim3((unsigned)((n + 255) / 256)), 256, 0, stream>>>(gate, up, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
+                             int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream) {
+    const int64_t nrows = (int64_t)n_used * ntok;
+    if (nrows == 0) return hipSuccess;
+    k_scale_rows<<<dim3((unsigned)((row_len + 255) / 256), (unsigned)nrows), 256, 0, stream>>>(x, row_len, n_used, nrows, w,
+                                                                                              w_s1, w_s2, x_s1, x_s2);
+    return hipGetLastError();
+}
+
+}  // namespace tq

@@ -33,6 +33,9 @@ struct GemvArgs {
     int32_t ncols;       // columns of this launch
     float *dst;          // dst of batch (0,0), column col0 is dst + col0*d_s1
     int64_t d_s1, d_s2, d_s3;  // float strides of dst
+    const float *b;      // when set: F32 activations, quantized to Q8_K inside each workgroup (q8 unused)
+    int64_t b_s1, b_s2, b_s3;  // float strides of b
+    int32_t b_vec;       // rows and strides 16-byte aligned
 };
 hipError_t launch_gemv(int type, const GemvArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
@@ -56,6 +59,31 @@ struct MmidArgs {
 };
 size_t mmid_route_bytes(int n_expert, int64_t n_slots);
 hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream);
+// decode-size routing (n_used * T <= 256): one launch, F32 activations quantized in each workgroup
+constexpr int64_t mmid_small_max_slots() { return 256; }
+hipError_t launch_mul_mat_id_small(int type, const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
+                                   hipStream_t stream);
+
+// The fused MoE expert FFN (gate, up, swiglu, down, router weight) for decode-size routing.
+struct MoeArgs {
+    const uint8_t *gate, *up, *down;   // stacked experts
+    int64_t g_s1, g_s2, u_s1, u_s2, dn_s1, dn_s2;  // bytes between rows / experts
+    int32_t n_embd, n_ff, n_expert, n_used, ntok;
+    const uint8_t *ids;
+    int64_t ids_s0, ids_s1;            // bytes
+    const float *b;                    // [n_embd, 1, T] activations
+    int64_t b_s2;                      // floats between tokens
+    int32_t b_vec;
+    const float *rw;                   // router weights [1, n_used, T] or null
+    int64_t rw_s1, rw_s2;              // floats
+    float *gu;                         // workspace: gate then up outputs, [2][n_slots][n_ff]
+    float *dst;                        // [n_embd, n_used, T]
+    int64_t o_s1, o_s2;                // floats
+};
+hipError_t launch_moe_ffn(int type_gate, int type_up, int type_down, const MoeArgs &m, hipStream_t stream);
+hipError_t launch_swiglu(const float *gate, const float *up, float *out, int64_t n, hipStream_t stream);
+hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
+                             int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream);
 
 // Device properties cached per device.
 int device_cu_count();

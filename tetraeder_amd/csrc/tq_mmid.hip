@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace tq {
 
@@ -151,6 +152,257 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_gemv(MmidArgs a) {
         else if (n <= 4) mmid_pass<F, 4, LPR>(a, w, slots, n, lds_qs, lds_bs, lds_d, col_dst);
         else mmid_pass<F, 8, LPR>(a, w, slots, n, lds_qs, lds_bs, lds_d, col_dst);
     }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Decode-size routing (n_used * T <= SMALL_MAX_SLOTS): no routing pass. grid.y walks the slots; the
+// workgroup of a slot owns its expert when the slot is the expert's first occurrence, gathers every
+// slot routed to that expert as its columns, quantizes their activation rows to Q8_K in LDS and
+// streams the expert once. Workgroups of later occurrences leave at once; slots with an id outside
+// [0, n_expert) get their zero row from the workgroup at grid.x = 0.
+// ------------------------------------------------------------------------------------------------
+constexpr int SMALL_MAX_SLOTS = 256;
+
+struct SlotGather {
+    int cols[SMALL_MAX_SLOTS];
+    int ncol, later;
+};
+
+// Expert of slot s when this workgroup owns it (cols/ncol filled), -1 when a lower slot owns it,
+// -2 when the id is outside [0, n_expert). Uniform over the workgroup.
+__device__ __forceinline__ int gather_slots(const uint8_t *ids, int64_t s0, int64_t s1, int n_used, int n_slots,
+                                            int n_expert, int s, SlotGather &g) {
+    const int e = load_id(ids, s0, s1, n_used, s);
+    if (e < 0 || e >= n_expert) return -2;
+    if (threadIdx.x == 0) g.ncol = 0, g.later = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_slots; i += blockDim.x) {
+        if (load_id(ids, s0, s1, n_used, i) != e) continue;
+        if (i < s) g.later = 1;
+        else g.cols[atomicAdd(&g.ncol, 1)] = i;
+    }
+    __syncthreads();
+    return g.later ? -1 : e;
+}
+
+template <int NC> using NCTag = std::integral_constant<int, NC>;
+
+// Streams one expert matrix against `cnt` columns, NC at a time: stage(NCTag<NC>, c0, n) fills the
+// LDS activations of columns c0 .. c0+n-1, dst_off(k) is the float offset of column k's output row,
+// store_scale(k) its multiplier.
+template <int F, int LPR, class Stage, class DstOff>
+__device__ __forceinline__ void expert_columns(const uint8_t *w, int nrows, int nb, uint32_t row_stride, float *dst,
+                                               int cnt, Stage stage, DstOff dst_off, uint8_t *lds) {
+    uint8_t *lds_qs = lds;
+    int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * 256);
+    float *lds_d = (float *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES));
+    int64_t *col_dst = (int64_t *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES + 4));
+    float *col_scale = (float *)(col_dst + MMID_NC);
+    auto pass = [&](auto nct, int c0, int n) {
+        constexpr int NC = decltype(nct)::value;
+        stage(nct, c0, n, lds_qs, lds_bs, lds_d);
+        if (threadIdx.x < NC) {
+            int64_t off = 0;
+            float sc = 0.f;
+            if ((int)threadIdx.x < n) dst_off(c0 + (int)threadIdx.x, off, sc);
+            col_dst[threadIdx.x] = off, col_scale[threadIdx.x] = sc;
+        }
+        __syncthreads();
+        gemv_rows<F, NC, LPR>(w, nrows, nb, row_stride, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
+                              gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, [&](int c, int row, float v) {
+                                  if (c < n) dst[col_dst[c] + row] = v * col_scale[c];
+                              });
+        __syncthreads();  // the next pass restages the same LDS
+    };
+    for (int c0 = 0; c0 < cnt; c0 += MMID_NC) {
+        const int n = min(MMID_NC, cnt - c0);
+        if (n == 1) pass(NCTag<1>(), c0, n);
+        else if (n == 2) pass(NCTag<2>(), c0, n);
+        else if (n <= 4) pass(NCTag<4>(), c0, n);
+        else pass(NCTag<8>(), c0, n);
+    }
+}
+
+template <int F, int LPR>
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_small(MmidArgs a, const float *b, int64_t b_s1, int64_t b_s2,
+                                                                int b_vec) {
+    __shared__ SlotGather g;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int s = blockIdx.y, n_slots = a.n_used * a.ntok;
+    const int e = gather_slots(a.ids, a.ids_s0, a.ids_s1, a.n_used, n_slots, a.n_expert, s, g);
+    if (e == -2) {
+        if (blockIdx.x == 0) {
+            float *row = a.dst + (s % a.n_used) * a.d_s1 + (s / a.n_used) * a.d_s2;
+            for (int i = threadIdx.x; i < a.nrows; i += blockDim.x) row[i] = 0.f;
+        }
+        return;
+    }
+    if (e < 0) return;
+    const int nb = a.nb;
+    auto stage = [&](auto nct, int c0, int n, uint8_t *qs, int16_t *bs, float *d) {
+        constexpr int NC = decltype(nct)::value;
+        stage_activations_f32<F, NC>(
+            [&](int k) {
+                const int sl = g.cols[c0 + k], j = sl % a.n_used, t = sl / a.n_used;
+                return b + t * b_s2 + (j % a.ne11) * b_s1;
+            },
+            b_vec != 0, nb, n, qs, bs, d);
+    };
+    auto dst_off = [&](int k, int64_t &off, float &sc) {
+        const int sl = g.cols[k];
+        off = (sl % a.n_used) * a.d_s1 + (sl / a.n_used) * a.d_s2, sc = 1.f;
+    };
+    expert_columns<F, LPR>(a.w + (int64_t)e * a.w_s2, a.nrows, nb, (uint32_t)a.w_s1, a.dst, g.ncol, stage, dst_off, lds);
+}
+
+// ------------------------------------------------------------------------------------------------
+// The MoE expert FFN of one layer (crates/model/src/qwen3moe.rs:2899-2914 weighted_experts):
+//   up = mul_mat_id(up_exps, cur, ids); gate = mul_mat_id(gate_exps, cur, ids);
+//   act = swiglu_split(gate, up) = silu(gate) * up; experts = mul_mat_id(down_exps, act, ids) * w.
+// Launch 1 (k_moe_gate_up, grid.z = gate/up): each routed expert's gate and up rows against its tokens,
+// outputs in fp32 to the workspace; zero rows of -1 slots in dst. Launch 2 (k_moe_down): per routed
+// expert, silu(gate) * up of each of its slots is formed and quantized to Q8_K in LDS (the Q8_K pass
+// the reference's down MUL_MAT_ID applies to act), then the down rows are streamed; each output row
+// is scaled by the slot's router weight when one is given.
+// ------------------------------------------------------------------------------------------------
+// z0 = 0 and grid.z = 2 runs gate and up (same type); z0 = 0 or 1 with grid.z = 1 runs one of them.
+template <int F, int LPR>
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_gate_up(MoeArgs m, int z0) {
+    __shared__ SlotGather g;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int s = blockIdx.y, n_slots = m.n_used * m.ntok, z = z0 + (int)blockIdx.z;
+    const int e = gather_slots(m.ids, m.ids_s0, m.ids_s1, m.n_used, n_slots, m.n_expert, s, g);
+    if (e == -2) {
+        if (blockIdx.x == 0 && z == 0) {
+            float *row = m.dst + (s % m.n_used) * m.o_s1 + (s / m.n_used) * m.o_s2;
+            for (int i = threadIdx.x; i < m.n_embd; i += blockDim.x) row[i] = 0.f;
+        }
+        return;
+    }
+    if (e < 0) return;
+    const int nb = m.n_embd / QK;
+    auto stage = [&](auto nct, int c0, int n, uint8_t *qs, int16_t *bs, float *d) {
+        constexpr int NC = decltype(nct)::value;
+        stage_activations_f32<F, NC>([&](int k) { return m.b + (g.cols[c0 + k] / m.n_used) * m.b_s2; }, m.b_vec != 0,
+                                     nb, n, qs, bs, d);
+    };
+    float *out = m.gu + (int64_t)z * n_slots * m.n_ff;
+    auto dst_off = [&](int k, int64_t &off, float &sc) { off = (int64_t)g.cols[k] * m.n_ff, sc = 1.f; };
+    const uint8_t *w = (z ? m.up : m.gate) + (int64_t)e * (z ? m.u_s2 : m.g_s2);
+    expert_columns<F, LPR>(w, m.n_ff, nb, (uint32_t)(z ? m.u_s1 : m.g_s1), out, g.ncol, stage, dst_off, lds);
+}
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+template <int F, int LPR>
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_down(MoeArgs m) {
+    __shared__ SlotGather g;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int s = blockIdx.y, n_slots = m.n_used * m.ntok;
+    const int e = gather_slots(m.ids, m.ids_s0, m.ids_s1, m.n_used, n_slots, m.n_expert, s, g);
+    if (e < 0) return;
+    const int nb = m.n_ff / QK;
+    auto stage = [&](auto nct, int c0, int n, uint8_t *qs, int16_t *bs, float *d) {
+        constexpr int NC = decltype(nct)::value;
+        const int wid = threadIdx.x >> 6, nw = blockDim.x >> 6, lane = lane_id();
+        for (int i = wid; i < n * nb; i += nw) {
+            const int k = i / nb, blk = i - k * nb;
+            const int64_t row = (int64_t)g.cols[c0 + k] * m.n_ff + blk * QK + 4 * lane;
+            const float4 gv = *(const float4 *)(m.gu + row);
+            const float4 uv = *(const float4 *)(m.gu + (int64_t)n_slots * m.n_ff + row);
+            const float v[4] = {silu_f32(gv.x) * uv.x, silu_f32(gv.y) * uv.y, silu_f32(gv.z) * uv.z,
+                                silu_f32(gv.w) * uv.w};
+            wave_quantize_vals_to_lds<F>(v, k * nb + blk, qs, bs, d);
+        }
+        for (int i = n * nb + threadIdx.x; i < NC * nb; i += blockDim.x) d[i] = 0.f;
+        for (int i = n * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x) ((uint32_t *)qs)[i] = 0;
+        for (int i = n * nb * 32 + threadIdx.x; i < NC * nb * 32; i += blockDim.x) bs[i] = 0;
+    };
+    auto dst_off = [&](int k, int64_t &off, float &sc) {
+        const int sl = g.cols[k], j = sl % m.n_used, t = sl / m.n_used;
+        off = j * m.o_s1 + t * m.o_s2;
+        sc = m.rw ? m.rw[j * m.rw_s1 + t * m.rw_s2] : 1.f;
+    };
+    expert_columns<F, LPR>(m.down + (int64_t)e * m.dn_s2, m.n_embd, nb, (uint32_t)m.dn_s1, m.dst, g.ncol, stage, dst_off,
+                           lds);
+}
+
+static int64_t expected_experts(int n_expert, int64_t n_slots) {
+    return std::max<int64_t>(1, (int64_t)std::ceil(n_expert * (1.0 - std::pow(1.0 - 1.0 / n_expert, (double)n_slots))));
+}
+
+static size_t expert_lds(int nb) { return (size_t)MMID_NC * nb * gemv_lds_per_col_block() + MMID_NC * 12; }
+
+template <int F, class Launch>
+static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int64_t n_slots, Launch launch) {
+    const int64_t slots = (int64_t)device_cu_count() * 32;
+    const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / expected_experts(n_expert, n_slots));
+    const int lpr = gemv_lanes_per_row(nb, nrows, per_expert);
+    const int64_t npass = (nrows + 64 / lpr - 1) / (64 / lpr);
+    const unsigned gx = (unsigned)((std::min<int64_t>(npass, per_expert) + GEMV_WAVES - 1) / GEMV_WAVES);
+    switch (lpr) {
+    case 8: launch(std::integral_constant<int, 8>(), gx); break;
+    case 16: launch(std::integral_constant<int, 16>(), gx); break;
+    case 32: launch(std::integral_constant<int, 32>(), gx); break;
+    default: launch(std::integral_constant<int, 64>(), gx); break;
+    }
+    return hipGetLastError();
+}
+
+template <int F>
+static hipError_t launch_small(const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
+                               hipStream_t stream) {
+    const int64_t n_slots = (int64_t)a.n_used * a.ntok;
+    return launch_expert_kernel<F>(a.nb, a.nrows, a.n_expert, n_slots, [&](auto lpr, unsigned gx) {
+        k_mmid_small<F, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(a.nb), stream>>>(
+            a, b, b_s1, b_s2, b_vec);
+    });
+}
+
+hipError_t launch_mul_mat_id_small(int type, const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
+                                   hipStream_t stream) {
+    return type == FMT_Q4K ? launch_small<FMT_Q4K>(a, b, b_s1, b_s2, b_vec, stream)
+                           : launch_small<FMT_Q6K>(a, b, b_s1, b_s2, b_vec, stream);
+}
+
+template <int FG, int FU, int FD>
+static hipError_t launch_moe_t(const MoeArgs &m, hipStream_t stream) {
+    const int64_t n_slots = (int64_t)m.n_used * m.ntok;
+    const int nb_in = m.n_embd / QK, nb_ff = m.n_ff / QK;
+    hipError_t e;
+    if (FG == FU) {
+        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+            k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 2), GEMV_WAVES * 64,
+                                                       expert_lds(nb_in), stream>>>(m, 0);
+        });
+    } else {
+        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+            k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
+                                                       expert_lds(nb_in), stream>>>(m, 0);
+        });
+        if (e == hipSuccess)
+            e = launch_expert_kernel<FU>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+                k_moe_gate_up<FU, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
+                                                           expert_lds(nb_in), stream>>>(m, 1);
+            });
+    }
+    if (e != hipSuccess) return e;
+    return launch_expert_kernel<FD>(nb_ff, m.n_embd, m.n_expert, n_slots, [&](auto lpr, unsigned gx) {
+        k_moe_down<FD, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(nb_ff), stream>>>(m);
+    });
+}
+
+template <int FG, int FU>
+static hipError_t launch_moe_d(int type_down, const MoeArgs &m, hipStream_t stream) {
+    return type_down == FMT_Q4K ? launch_moe_t<FG, FU, FMT_Q4K>(m, stream) : launch_moe_t<FG, FU, FMT_Q6K>(m, stream);
+}
+
+hipError_t launch_moe_ffn(int type_gate, int type_up, int type_down, const MoeArgs &m, hipStream_t stream) {
+    if (type_gate == FMT_Q4K)
+        return type_up == FMT_Q4K ? launch_moe_d<FMT_Q4K, FMT_Q4K>(type_down, m, stream)
+                                  : launch_moe_d<FMT_Q4K, FMT_Q6K>(type_down, m, stream);
+    return type_up == FMT_Q4K ? launch_moe_d<FMT_Q6K, FMT_Q4K>(type_down, m, stream)
+                              : launch_moe_d<FMT_Q6K, FMT_Q6K>(type_down, m, stream);
 }
 
 template <int F>

@@ -201,6 +201,34 @@ def mul_mat_id_workspace_size(experts: QTensor, b: torch.Tensor, ids: torch.Tens
     return int(_lib.lib().tq_mul_mat_id_workspace_size(C.byref(at), C.byref(bt), C.byref(it)))
 
 
+def moe_ffn(gate: QTensor, up: QTensor, down: QTensor, b: torch.Tensor, ids: torch.Tensor,
+            weights: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """The MoE expert FFN (weighted_experts, crates/model/src/qwen3moe.rs:2899-2914):
+    down(swiglu(gate(b), up(b))) per routed slot, times the router weight.
+    b float32 torch [T, 1, n_embd], ids int32 [T, n_used], weights float32 [T, n_used, 1] or None;
+    returns [T, n_used, n_embd]."""
+    if b.dtype != torch.float32 or ids.dtype != torch.int32 or b.dim() != 3 or ids.dim() != 2:
+        raise Invalid("b is float32 [T, 1, n_embd] and ids int32 [T, n_used]")
+    T, n_used = ids.shape
+    if out is None:
+        out = torch.empty((T, n_used, gate.ne[0]), dtype=torch.float32, device=b.device)
+    gt, ut, dt_, bt, it, ot = gate.raw(), up.raw(), down.raw(), _dense(b, Type.F32), _dense(ids, Type.I32), \
+        _dense(out, Type.F32)
+    wt = C.byref(_dense(weights, Type.F32)) if weights is not None else None
+    ws_ptr, ws_size = 0, 0
+    if workspace is not None:
+        ws_ptr, ws_size = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    _check(_lib.lib().tq_moe_ffn(C.byref(gt), C.byref(ut), C.byref(dt_), C.byref(bt), C.byref(it), wt, C.byref(ot),
+                                 ws_ptr, ws_size, _stream(stream)))
+    return out
+
+
+def moe_ffn_workspace_size(gate: QTensor, b: torch.Tensor, ids: torch.Tensor) -> int:
+    gt, bt, it = gate.raw(), _dense(b, Type.F32), _dense(ids, Type.I32)
+    return int(_lib.lib().tq_moe_ffn_workspace_size(C.byref(gt), C.byref(bt), C.byref(it)))
+
+
 def to_f32(ty: Type, src: torch.Tensor, n: int, stream=None) -> torch.Tensor:
     """Dequantizes n elements (whole blocks of ty) from a uint8 device buffer."""
     if src.numel() < ty.row_size(n):
