@@ -39,7 +39,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
-    p.add_argument("--only", choices=["gemv", "copy"], default=None,
+    p.add_argument("--only", choices=["gemv", "copy", "moe"], default=None,
                    help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
                         "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
     return p.parse_args()
@@ -145,6 +145,9 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copied {args.steps} x 256 MiB")
+        return
+    if args.only == "moe":
+        print(json.dumps(bench_moe(ggml, torch, np, dev)))
         return
 
     # ---- headline: Q6_K output head 151936 x 2048, batch 1 ----

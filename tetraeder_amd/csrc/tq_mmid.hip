@@ -333,10 +333,12 @@ static int64_t expected_experts(int n_expert, int64_t n_slots) {
 
 static size_t expert_lds(int nb) { return (size_t)MMID_NC * nb * gemv_lds_per_col_block() + MMID_NC * 12; }
 
+// Sizes an expert kernel's grid.x: the resident wave slots shared among the expected routed experts
+// (uniform routing of n_slots slots) times `mats` matrices per expert.
 template <int F, class Launch>
-static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int64_t n_slots, Launch launch) {
+static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int64_t n_slots, int mats, Launch launch) {
     const int64_t slots = (int64_t)device_cu_count() * 32;
-    const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / expected_experts(n_expert, n_slots));
+    const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / (mats * expected_experts(n_expert, n_slots)));
     const int lpr = gemv_lanes_per_row(nb, nrows, per_expert);
     const int64_t npass = (nrows + 64 / lpr - 1) / (64 / lpr);
     const unsigned gx = (unsigned)((std::min<int64_t>(npass, per_expert) + GEMV_WAVES - 1) / GEMV_WAVES);
@@ -353,7 +355,7 @@ template <int F>
 static hipError_t launch_small(const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
                                hipStream_t stream) {
     const int64_t n_slots = (int64_t)a.n_used * a.ntok;
-    return launch_expert_kernel<F>(a.nb, a.nrows, a.n_expert, n_slots, [&](auto lpr, unsigned gx) {
+    return launch_expert_kernel<F>(a.nb, a.nrows, a.n_expert, n_slots, 1, [&](auto lpr, unsigned gx) {
         k_mmid_small<F, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(a.nb), stream>>>(
             a, b, b_s1, b_s2, b_vec);
     });
@@ -371,23 +373,23 @@ static hipError_t launch_moe_t(const MoeArgs &m, hipStream_t stream) {
     const int nb_in = m.n_embd / QK, nb_ff = m.n_ff / QK;
     hipError_t e;
     if (FG == FU) {
-        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
             k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 2), GEMV_WAVES * 64,
                                                        expert_lds(nb_in), stream>>>(m, 0);
         });
     } else {
-        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
             k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
                                                        expert_lds(nb_in), stream>>>(m, 0);
         });
         if (e == hipSuccess)
-            e = launch_expert_kernel<FU>(nb_in, m.n_ff, m.n_expert, 2 * n_slots, [&](auto lpr, unsigned gx) {
+            e = launch_expert_kernel<FU>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
                 k_moe_gate_up<FU, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
                                                            expert_lds(nb_in), stream>>>(m, 1);
             });
     }
     if (e != hipSuccess) return e;
-    return launch_expert_kernel<FD>(nb_ff, m.n_embd, m.n_expert, n_slots, [&](auto lpr, unsigned gx) {
+    return launch_expert_kernel<FD>(nb_ff, m.n_embd, m.n_expert, n_slots, 1, [&](auto lpr, unsigned gx) {
         k_moe_down<FD, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(nb_ff), stream>>>(m);
     });
 }
