@@ -186,10 +186,16 @@ def main():
     achieved = wbytes / (kern_us * 1e-6) / 1e9
     log(f"gemv kernel {kern_us:.2f} us -> {achieved:.1f} GB/s")
 
+    # HBM bytes per launch: rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel, each scaled by what the
+    # counter reads for a plain copy of known size (the profile summary next to traffic.json says how)
     traffic = None
+    traffic_ratio = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("gemv_q6_K_151936x2048_m1")
+        rec = json.load(open(tpath)).get("gemv_q6_K_151936x2048_m1")
+        if rec:
+            traffic = int(rec["bytes"])
+            traffic_ratio = round(traffic / wbytes, 4)
 
     cpu = None
     if not args.no_cpu:
@@ -225,6 +231,7 @@ def main():
                                "2 rotated weight copies", "n": n, "k": k, "batch": 1, "weight_bytes": wbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_over_algorithmic": traffic_ratio,
                      "kernel": "k_gemv<q6_K,1 col>", "kernel_us": round(kern_us, 2)},
         "cpu_baseline": cpu,
         "moe_mul_mat_id_us_per_token": {t: v["us_per_token"] for t, v in moe.items()},
