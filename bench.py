@@ -39,7 +39,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
-    p.add_argument("--only", choices=["gemv", "copy", "moe"], default=None,
+    p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill"], default=None,
                    help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
                         "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
     return p.parse_args()
@@ -149,6 +149,9 @@ def main():
     if args.only == "moe":
         print(json.dumps(bench_moe(ggml, torch, np, dev)))
         return
+    if args.only == "prefill":
+        print(json.dumps(bench_prefill(ggml, torch, dev, only=os.environ.get("TQ_BENCH_PROFILE") == "1")))
+        return
 
     # ---- headline: Q6_K output head 151936 x 2048, batch 1 ----
     ty, k, n = ggml.Type.Q6_K, 2048, 151936
@@ -221,6 +224,7 @@ def main():
         moe = bench_moe(ggml, torch, np, dev)
         secondary["moe_step"] = moe
         secondary.update(bench_secondary(ggml, torch, dev))
+        secondary["prefill"] = bench_prefill(ggml, torch, dev)
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -286,6 +290,42 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8):
         log(f"moe T={T}: {res[str(T)]}")
     del L
     torch.cuda.empty_cache()
+    return res
+
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def bench_prefill(ggml, torch, dev, only=False):
+    """Dense prefill GEMMs (hidden 4096, FFN 12288): Q4_K gate/up [4096 -> 12288] and Q6_K down
+    [12288 -> 4096] at M = 512 and 2048 activation rows. op = MUL_MAT with the F32 activations (Q8_K
+    pass included); kernel = the MFMA kernel alone on pre-quantized activations. int ops = 2 M N K."""
+    res = {}
+    shapes = (("gate_up", ggml.Type.Q4_K, 4096, 12288), ("down", ggml.Type.Q6_K, 12288, 4096))
+    for name, ty, k, n in shapes:
+        W = make_weights(ggml, torch, ty, k, n, 2, seed=k + n, dev=dev)
+        for m in (512, 2048):
+            x = torch.randn((m, k), device=dev)
+            out = torch.empty((m, n), device=dev)
+            ws = torch.empty(ggml.mul_mat_workspace_size(W[0], x), dtype=torch.uint8, device=dev)
+            xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
+            if only:
+                for i in range(20):
+                    ggml.mul_mat(W[i & 1], xq, out=out)
+                torch.cuda.synchronize()
+                continue
+            op_us = time_launches(torch, lambda i: ggml.mul_mat(W[i & 1], x, out=out, workspace=ws), 20)
+            kern_us = time_launches(torch, lambda i: ggml.mul_mat(W[i & 1], xq, out=out), 20)
+            ops = 2.0 * m * n * k
+            res[f"{name}_{ty.name}_{k}x{n}_m{m}"] = {
+                "op_us": round(op_us, 1), "kernel_us": round(kern_us, 1),
+                "kernel_TOPS": round(ops / kern_us / 1e6, 1),
+                "mfma_frac": round(ops / kern_us / 1e6 / PEAK_INT8_TOPS, 4),
+                "op_TOPS": round(ops / op_us / 1e6, 1)}
+            log(f"prefill {name} m={m}: {res[f'{name}_{ty.name}_{k}x{n}_m{m}']}")
+            del x, out, ws, xq
+        del W
+        torch.cuda.empty_cache()
     return res
 
 

@@ -130,7 +130,14 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Decode-size activations (at most two Q8_K blocks per wave of a GEMV workgroup) are quantized by each
 // workgroup into LDS: one launch instead of two. Larger ones get a quantization pass of their own.
-static bool quantize_in_workgroup(int64_t ncols, int nb) { return ncols * nb <= 16; }
+// Columns from which MUL_MAT runs on the int8-MFMA kernel (all columns in one pass over the weights)
+// instead of the streaming GEMV (at most 8 columns per pass).
+constexpr int64_t MMQ_MIN_COLS = 9;
+
+static bool use_mmq(int64_t ncols) { return ncols >= MMQ_MIN_COLS; }
+
+// Decode-size F32 activations are quantized inside the GEMV workgroups (no workspace, one launch).
+static bool quantize_in_workgroup(int64_t ncols, int nb) { return !use_mmq(ncols) && ncols * nb <= 16; }
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
 
@@ -192,8 +199,10 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
     if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
     const int nb = (int)(a->ne[0] / QK);
+    const bool mmq = use_mmq(b->ne[1]);
     const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
-    if (nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
+    if (!mmq && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
+    if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
 
     hipStream_t s = (hipStream_t)stream;
     void *q8 = b->data;
@@ -210,6 +219,26 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
                                                  b->nb[2], b->nb[3], q8, s),
                             "quantize_q8_K launch")))
             return rc;
+    }
+    if (mmq) {
+        MmqArgs m{};
+        m.w = (const uint8_t *)a->data;
+        m.nrows = a->ne[1];
+        m.nb = nb;
+        m.row_stride = (int64_t)a->nb[1];
+        m.w_s2 = (int64_t)a->nb[2];
+        m.w_s3 = (int64_t)a->nb[3];
+        m.r2 = (int32_t)(b->ne[2] / a->ne[2]);
+        m.r3 = (int32_t)(b->ne[3] / a->ne[3]);
+        m.ne12 = (int32_t)b->ne[2];
+        m.nbatch = (int32_t)(b->ne[2] * b->ne[3]);
+        m.q8 = (const uint8_t *)q8;
+        m.ncols = (int32_t)b->ne[1];
+        m.dst = (float *)dst->data;
+        m.d_s1 = (int64_t)(dst->nb[1] / 4);
+        m.d_s2 = (int64_t)(dst->nb[2] / 4);
+        m.d_s3 = (int64_t)(dst->nb[3] / 4);
+        return check_hip(launch_mmq(a->type, m, s), "mmq launch");
     }
     GemvArgs g{};
     g.w = (const uint8_t *)a->data;

@@ -38,6 +38,23 @@ struct GemvArgs {
     int32_t b_vec;       // rows and strides 16-byte aligned
 };
 hipError_t launch_gemv(int type, const GemvArgs &a, hipStream_t stream);
+
+// MUL_MAT on int8 MFMA for many columns: every Q8_K column of a batch at once, any K (multiple of 256).
+struct MmqArgs {
+    const uint8_t *w;    // weights of batch (0,0)
+    int64_t nrows;       // N
+    int32_t nb;          // super-blocks per row (K/256)
+    int64_t row_stride;  // bytes between rows
+    int64_t w_s2, w_s3;  // bytes between weight matrices in dims 2, 3
+    int32_t r2, r3;      // broadcast ratios ne12/ne02, ne13/ne03
+    int32_t ne12;        // batch extent of dim 2
+    int32_t nbatch;      // ne12*ne13 (grid.y)
+    const uint8_t *q8;   // Q8_K rows; column m of batch z at q8 + (z*ncols + m)*nb*292 (4-byte aligned)
+    int32_t ncols;       // M
+    float *dst;          // dst[m*d_s1 + n] of batch (i2,i3) at dst + i2*d_s2 + i3*d_s3
+    int64_t d_s1, d_s2, d_s3;  // float strides
+};
+hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }
 
