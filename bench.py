@@ -39,6 +39,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--moe-tokens", type=int, default=0, help="with --only moe: run just this token count")
     p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill"], default=None,
                    help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
                         "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
@@ -147,7 +148,7 @@ def main():
         log(f"copied {args.steps} x 256 MiB")
         return
     if args.only == "moe":
-        print(json.dumps(bench_moe(ggml, torch, np, dev)))
+        print(json.dumps(bench_moe(ggml, torch, np, dev, tokens=(args.moe_tokens,) if args.moe_tokens else None)))
         return
     if args.only == "prefill":
         print(json.dumps(bench_prefill(ggml, torch, dev, only=os.environ.get("TQ_BENCH_PROFILE") == "1")))
@@ -258,7 +259,7 @@ def moe_ids(np, tokens, seed, n_expert=128, used=8, neg_frac=0.1):
     return ids
 
 
-def bench_moe(ggml, torch, np, dev, layers=4, routings=8):
+def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
     """The MoE expert FFN step (gate, up, swiglu, down) at Qwen3-30B-A3B shapes: 128 experts, n_embd
     2048, n_ff 768, gate/up Q4_K, down Q6_K, top-8 with 10% -1. Steps rotate over `layers` weight copies
     (4 x 392 MB) and `routings` seeded id sets, captured in a HIP graph; the roofline bytes are the
@@ -271,7 +272,7 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8):
                                                        (ggml.Type.Q6_K, n_ff, n_embd)))))
     L = [tuple(ggml.QTensor(w.type, (w.ne[0], w.ne[1] // E, E), w.data) for w in lw) for lw in L]
     res = {}
-    for T in (1, 2, 4, 8, 16):
+    for T in tokens or (1, 2, 4, 8, 16):
         ids_np = [moe_ids(np, T, seed=1000 * T + r) for r in range(routings)]
         uniq = [len(set(int(e) for e in x.reshape(-1) if e >= 0)) for x in ids_np]
         ids = [torch.from_numpy(x).to(dev) for x in ids_np]

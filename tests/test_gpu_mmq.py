@@ -1,8 +1,9 @@
-"""MUL_MAT with 9 or more activation columns (the int8-MFMA kernel) on the GPU against the oracle.
+"""MUL_MAT with many activation columns on the GPU against the oracle: 64 or more columns run on the
+int8-MFMA kernel, fewer on the streaming GEMV (8 columns per pass); the cases straddle the switch.
 
 Same bar as the GEMV: every output within 1e-3 of the largest reference magnitude (fp32 accumulation
 order is the only difference: both sides use the same weight bytes and the same Q8_K activations).
-Covers ragged M and N around the 32 x 128 / 64 x 128 / 128 x 64 tile edges, K from one super-block to
+Covers ragged M and N around the 64 x 128 / 128 x 64 / 256 x 64 tile edges, K from one super-block to
 12288, broadcast over dims 2 and 3 with strided b and dst, a pre-quantized Q8_K b, activations with a
 huge dynamic range and all-zero columns, and the dense prefill shapes (hidden 4096, FFN 12288, Q4_K
 gate/up and Q6_K down at M = 512 and 2048) on sampled weight rows.
@@ -59,7 +60,7 @@ def test_mmq_broadcast_and_strides(gpu, tname):
     """a [K, N, 2] broadcast over b [K, M, 4] (i02 = i12 / 2); b rows strided; dst a strided view."""
     _case(f"{tname} broadcast")
     ty = TYPES[tname]
-    k, n, m = 512, 70, 40
+    k, n, m = 512, 70, 72
     w = make_weights(ty, k, n, 2, seed=55, device=gpu)
     xb = normal((4, m, k + 64), 56)
     xt = torch.from_numpy(xb).to(gpu)[:, :, 32:32 + k]
@@ -77,7 +78,7 @@ def test_mmq_prequantized_b(gpu, tname):
     """b already Q8_K (ggml's vec_dot_type) gives the same result as the F32 b it came from."""
     _case(f"{tname} q8_K b")
     ty = TYPES[tname]
-    k, n, m = 1024, 96, 48
+    k, n, m = 1024, 96, 96
     w = make_weights(ty, k, n, 1, seed=3, device=gpu)
     x = torch.from_numpy(normal((m, k), 4)).to(gpu)
     xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
@@ -91,7 +92,7 @@ def test_mmq_dynamic_range_and_zero_columns(gpu, tname):
     """Columns scaled over 1e-30 .. 1e30 and all-zero columns (Q8_K d = 0)."""
     _case(f"{tname} dynamic range")
     ty = TYPES[tname]
-    k, n, m = 768, 64, 24
+    k, n, m = 768, 64, 80
     w = make_weights(ty, k, n, 1, seed=8, device=gpu)
     x = normal((m, k), 9)
     x *= (10.0 ** np.linspace(-30, 30, m)).astype(np.float32)[:, None]
@@ -108,9 +109,9 @@ def test_mmq_dynamic_range_and_zero_columns(gpu, tname):
 def test_mmq_workspace_argument(gpu):
     _case("workspace")
     w = make_weights(ggml.Type.Q6_K, 1024, 64, 1, seed=7, device=gpu)
-    x = torch.from_numpy(normal((40, 1024), 9)).to(gpu)
+    x = torch.from_numpy(normal((80, 1024), 9)).to(gpu)
     need = ggml.mul_mat_workspace_size(w, x)
-    assert need >= 40 * 4 * 292
+    assert need >= 80 * 4 * 292
     ws = torch.empty(need, dtype=torch.uint8, device=gpu)
     a = ggml.mul_mat(w, x, workspace=ws)
     b = ggml.mul_mat(w, x)

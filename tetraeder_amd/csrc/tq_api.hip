@@ -5,6 +5,8 @@
 #include "tq_internal.h"
 
 #include <algorithm>
+#include <map>
+#include <tuple>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -42,6 +44,24 @@ int device_cu_count() {
         cus[dev] = n;
     }
     return cus[dev];
+}
+
+// Waves of `kernel` (launched with `threads` per workgroup and `lds` dynamic LDS bytes) that one CU holds
+// at once, from the kernel's register and LDS use; cached per device, kernel and LDS size.
+int resident_waves_per_cu(const void *kernel, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void *, size_t>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    const auto key = std::make_tuple(dev, kernel, lds);
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int nblk = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nblk, kernel, threads, lds) != hipSuccess || nblk < 1) nblk = 1;
+    const int w = nblk * std::max(1, threads / 64);
+    cache[key] = w;
+    return w;
 }
 
 // Grow-only per-device workspace for callers that pass none (allocates on growth: not capture-safe).
@@ -131,8 +151,9 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // Decode-size activations (at most two Q8_K blocks per wave of a GEMV workgroup) are quantized by each
 // workgroup into LDS: one launch instead of two. Larger ones get a quantization pass of their own.
 // Columns from which MUL_MAT runs on the int8-MFMA kernel (all columns in one pass over the weights)
-// instead of the streaming GEMV (at most 8 columns per pass).
-constexpr int64_t MMQ_MIN_COLS = 9;
+// instead of the streaming GEMV (at most 8 columns per pass); below it the GEMV's shorter dependency
+// chain wins on decode shapes.
+constexpr int64_t MMQ_MIN_COLS = 64;
 
 static bool use_mmq(int64_t ncols) { return ncols >= MMQ_MIN_COLS; }
 

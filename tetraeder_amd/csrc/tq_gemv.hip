@@ -19,21 +19,23 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
     uint8_t *lds_qs = lds;
     int16_t *lds_bs = (int16_t *)(lds + NC * nb * 256);
     float *lds_d = (float *)(lds + NC * nb * (256 + ACT_BS_BYTES));
-    if (a.b) {
-        const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;
-        const int64_t b_s1 = a.b_s1;
-        stage_activations_f32<F, NC>([&](int c) { return b + c * b_s1; }, a.b_vec != 0, nb, a.ncols, lds_qs, lds_bs,
-                                     lds_d);
-    } else {
-        const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
-        stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
-    }
-    __syncthreads();
+    auto stage = [&]() {
+        if (a.b) {
+            const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;
+            const int64_t b_s1 = a.b_s1;
+            stage_activations_f32<F, NC>([&](int c) { return b + c * b_s1; }, a.b_vec != 0, nb, a.ncols, lds_qs,
+                                         lds_bs, lds_d);
+        } else {
+            const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
+            stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
+        }
+        __syncthreads();
+    };
 
     const int ncols = a.ncols;
     const int64_t d_s1 = a.d_s1;
     gemv_rows<F, NC, LPR>(w, (int)a.nrows, nb, (uint32_t)a.row_stride, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
-                          gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, [&](int c, int row, float v) {
+                          gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, stage, [&](int c, int row, float v) {
                               if (c < ncols) dst[c * d_s1 + row] = v;
                           });
 }
@@ -49,13 +51,15 @@ int gemv_lanes_per_row(int nb, int64_t nrows, int64_t slots) {
 
 template <int F, int NC>
 static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
-    const int64_t slots = (int64_t)device_cu_count() * 32;
+    const size_t lds = (size_t)NC * a.nb * gemv_lds_per_col_block();
+    // resident wave slots of the GPU for this kernel (registers and LDS permitting)
+    const int64_t slots = (int64_t)device_cu_count() * resident_waves_per_cu((const void *)k_gemv<F, NC, 16>,
+                                                                              GEMV_WAVES * 64, lds);
     const int lpr = gemv_lanes_per_row(a.nb, a.nrows, slots);
     const int rpw = 64 / lpr;
     const int64_t npass = (a.nrows + rpw - 1) / rpw;
     const int64_t waves = std::min<int64_t>(npass, slots);
     const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
-    const size_t lds = (size_t)NC * a.nb * gemv_lds_per_col_block();
     switch (lpr) {
     case 8: k_gemv<F, NC, 8><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
     case 16: k_gemv<F, NC, 16><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;

@@ -274,16 +274,19 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
 // Streams rows [0, nrows) of one weight matrix (nb super-blocks per row, row_stride bytes apart) against
 // the NC columns staged in LDS; this wave takes passes wave, wave + nwaves, ... of 64/LPR rows each.
 // store(c, row, value) receives every row total of column c (called by one lane per row and column).
-template <int F, int NC, int LPR, class Store>
+// stage() runs on every wave of the workgroup after the wave's first weight loads are issued and
+// before the first item is computed: it fills the LDS columns (and ends with a workgroup barrier), so
+// the activation staging overlaps the weights' memory latency.
+template <int F, int NC, int LPR, class Stage, class Store>
 __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nrows, int nb, uint32_t row_stride, int wave,
                                           int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs, const float *lds_d,
-                                          Store store) {
+                                          Stage stage, Store store) {
     constexpr int G = LPR / 8;     // super-blocks of a row in flight per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     const int lane = lane_id();
     const int u = lane & 7, gb = (lane % LPR) >> 3, lrow = lane / LPR, lir = lane % LPR;
     const int npass = (nrows + RPW - 1) / RPW;
-    if (wave >= npass) return;
+    const bool active = wave < npass;  // uniform over the wave
 
     // Wave passes are interleaved over the matrix (pass wave, wave + nwaves, ...), so at any moment the
     // resident waves read one contiguous stretch of rows: HBM streams best that way. The lane walks
@@ -334,7 +337,9 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nro
         return more;
     };
     Item<F> A, B;
-    load(A, cur);
+    if (active) load(A, cur);
+    stage();
+    if (!active) return;
     for (;;) {
         if (!step(A, B)) break;
         if (!step(B, A)) break;

@@ -104,5 +104,7 @@ hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok
 
 // Device properties cached per device.
 int device_cu_count();
+// Waves of a kernel one CU holds at once (register and LDS limits), for sizing streaming grids.
+int resident_waves_per_cu(const void *kernel, int threads, size_t lds);
 
 }  // namespace tq

@@ -106,24 +106,26 @@ __device__ __forceinline__ void mmid_pass(const MmidArgs &a, const uint8_t *w, c
                                           uint8_t *lds_qs, int16_t *lds_bs, float *lds_d, int64_t *col_dst) {
     const int nb = a.nb;
     const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
-    stage_activations<F, NC>(
-        [&](int c) {
-            const int s = slots[c], j = s % a.n_used, t = s / a.n_used;
-            return a.q8 + ((int64_t)t * a.ne11 + j % a.ne11) * col_bytes;
-        },
-        nb, ncols, lds_qs, lds_bs, lds_d);
-    if (threadIdx.x < NC) {
-        int64_t off = 0;
-        if ((int)threadIdx.x < ncols) {
-            const int s = slots[threadIdx.x], j = s % a.n_used, t = s / a.n_used;
-            off = j * a.d_s1 + t * a.d_s2;
+    auto stage = [&]() {
+        stage_activations<F, NC>(
+            [&](int c) {
+                const int s = slots[c], j = s % a.n_used, t = s / a.n_used;
+                return a.q8 + ((int64_t)t * a.ne11 + j % a.ne11) * col_bytes;
+            },
+            nb, ncols, lds_qs, lds_bs, lds_d);
+        if (threadIdx.x < NC) {
+            int64_t off = 0;
+            if ((int)threadIdx.x < ncols) {
+                const int s = slots[threadIdx.x], j = s % a.n_used, t = s / a.n_used;
+                off = j * a.d_s1 + t * a.d_s2;
+            }
+            col_dst[threadIdx.x] = off;
         }
-        col_dst[threadIdx.x] = off;
-    }
-    __syncthreads();
+        __syncthreads();
+    };
     float *dst = a.dst;
     gemv_rows<F, NC, LPR>(w, a.nrows, nb, (uint32_t)a.w_s1, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
-                          gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, [&](int c, int row, float v) {
+                          gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, stage, [&](int c, int row, float v) {
                               if (c < ncols) dst[col_dst[c] + row] = v;
                           });
     __syncthreads();  // the next pass restages the same LDS
@@ -190,9 +192,10 @@ template <int NC> using NCTag = std::integral_constant<int, NC>;
 // Streams one expert matrix against `cnt` columns, NC at a time: stage(NCTag<NC>, c0, n) fills the
 // LDS activations of columns c0 .. c0+n-1, dst_off(k) is the float offset of column k's output row,
 // store_scale(k) its multiplier.
-template <int F, int LPR, class Stage, class DstOff>
+template <int F, int LPR, int NCM, class Stage, class DstOff>
 __device__ __forceinline__ void expert_columns(const uint8_t *w, int nrows, int nb, uint32_t row_stride, float *dst,
                                                int cnt, Stage stage, DstOff dst_off, uint8_t *lds) {
+    static_assert(NCM == 1 || NCM == 2 || NCM == 4 || NCM == 8, "columns per pass");
     uint8_t *lds_qs = lds;
     int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * 256);
     float *lds_d = (float *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES));
@@ -200,30 +203,33 @@ __device__ __forceinline__ void expert_columns(const uint8_t *w, int nrows, int 
     float *col_scale = (float *)(col_dst + MMID_NC);
     auto pass = [&](auto nct, int c0, int n) {
         constexpr int NC = decltype(nct)::value;
-        stage(nct, c0, n, lds_qs, lds_bs, lds_d);
-        if (threadIdx.x < NC) {
-            int64_t off = 0;
-            float sc = 0.f;
-            if ((int)threadIdx.x < n) dst_off(c0 + (int)threadIdx.x, off, sc);
-            col_dst[threadIdx.x] = off, col_scale[threadIdx.x] = sc;
-        }
-        __syncthreads();
+        auto pre = [&]() {
+            stage(nct, c0, n, lds_qs, lds_bs, lds_d);
+            if (threadIdx.x < NC) {
+                int64_t off = 0;
+                float sc = 0.f;
+                if ((int)threadIdx.x < n) dst_off(c0 + (int)threadIdx.x, off, sc);
+                col_dst[threadIdx.x] = off, col_scale[threadIdx.x] = sc;
+            }
+            __syncthreads();
+        };
         gemv_rows<F, NC, LPR>(w, nrows, nb, row_stride, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
-                              gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, [&](int c, int row, float v) {
+                              gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, pre, [&](int c, int row, float v) {
                                   if (c < n) dst[col_dst[c] + row] = v * col_scale[c];
                               });
         __syncthreads();  // the next pass restages the same LDS
     };
-    for (int c0 = 0; c0 < cnt; c0 += MMID_NC) {
-        const int n = min(MMID_NC, cnt - c0);
-        if (n == 1) pass(NCTag<1>(), c0, n);
-        else if (n == 2) pass(NCTag<2>(), c0, n);
-        else if (n <= 4) pass(NCTag<4>(), c0, n);
-        else pass(NCTag<8>(), c0, n);
+    // NCM bounds the columns per pass (and so the registers of the kernel); more columns take more passes
+    for (int c0 = 0; c0 < cnt; c0 += NCM) {
+        const int n = min(NCM, cnt - c0);
+        if (NCM == 1 || n == 1) pass(NCTag<1>(), c0, n);
+        else if (NCM == 2 || n == 2) pass(NCTag<NCM == 1 ? 1 : 2>(), c0, n);
+        else if (NCM == 4 || n <= 4) pass(NCTag<NCM <= 2 ? NCM : 4>(), c0, n);
+        else pass(NCTag<NCM>(), c0, n);
     }
 }
 
-template <int F, int LPR>
+template <int F, int LPR, int NCM>
 __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_small(MmidArgs a, const float *b, int64_t b_s1, int64_t b_s2,
                                                                 int b_vec) {
     __shared__ SlotGather g;
@@ -252,7 +258,8 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_small(MmidArgs a, cons
         const int sl = g.cols[k];
         off = (sl % a.n_used) * a.d_s1 + (sl / a.n_used) * a.d_s2, sc = 1.f;
     };
-    expert_columns<F, LPR>(a.w + (int64_t)e * a.w_s2, a.nrows, nb, (uint32_t)a.w_s1, a.dst, g.ncol, stage, dst_off, lds);
+    expert_columns<F, LPR, NCM>(a.w + (int64_t)e * a.w_s2, a.nrows, nb, (uint32_t)a.w_s1, a.dst, g.ncol, stage, dst_off,
+                                lds);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -266,7 +273,7 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_small(MmidArgs a, cons
 // is scaled by the slot's router weight when one is given.
 // ------------------------------------------------------------------------------------------------
 // z0 = 0 and grid.z = 2 runs gate and up (same type); z0 = 0 or 1 with grid.z = 1 runs one of them.
-template <int F, int LPR>
+template <int F, int LPR, int NCM>
 __global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_gate_up(MoeArgs m, int z0) {
     __shared__ SlotGather g;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -289,12 +296,12 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_gate_up(MoeArgs m, int 
     float *out = m.gu + (int64_t)z * n_slots * m.n_ff;
     auto dst_off = [&](int k, int64_t &off, float &sc) { off = (int64_t)g.cols[k] * m.n_ff, sc = 1.f; };
     const uint8_t *w = (z ? m.up : m.gate) + (int64_t)e * (z ? m.u_s2 : m.g_s2);
-    expert_columns<F, LPR>(w, m.n_ff, nb, (uint32_t)(z ? m.u_s1 : m.g_s1), out, g.ncol, stage, dst_off, lds);
+    expert_columns<F, LPR, NCM>(w, m.n_ff, nb, (uint32_t)(z ? m.u_s1 : m.g_s1), out, g.ncol, stage, dst_off, lds);
 }
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-template <int F, int LPR>
+template <int F, int LPR, int NCM>
 __global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_down(MoeArgs m) {
     __shared__ SlotGather g;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -323,8 +330,8 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_down(MoeArgs m) {
         off = j * m.o_s1 + t * m.o_s2;
         sc = m.rw ? m.rw[j * m.rw_s1 + t * m.rw_s2] : 1.f;
     };
-    expert_columns<F, LPR>(m.down + (int64_t)e * m.dn_s2, m.n_embd, nb, (uint32_t)m.dn_s1, m.dst, g.ncol, stage, dst_off,
-                           lds);
+    expert_columns<F, LPR, NCM>(m.down + (int64_t)e * m.dn_s2, m.n_embd, nb, (uint32_t)m.dn_s1, m.dst, g.ncol, stage,
+                                dst_off, lds);
 }
 
 static int64_t expected_experts(int n_expert, int64_t n_slots) {
@@ -333,32 +340,55 @@ static int64_t expected_experts(int n_expert, int64_t n_slots) {
 
 static size_t expert_lds(int nb) { return (size_t)MMID_NC * nb * gemv_lds_per_col_block() + MMID_NC * 12; }
 
-// Sizes an expert kernel's grid.x: the resident wave slots shared among the expected routed experts
-// (uniform routing of n_slots slots) times `mats` matrices per expert.
-template <int F, class Launch>
-static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int64_t n_slots, int mats, Launch launch) {
-    const int64_t slots = (int64_t)device_cu_count() * 32;
-    const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / (mats * expected_experts(n_expert, n_slots)));
-    const int lpr = gemv_lanes_per_row(nb, nrows, per_expert);
-    const int64_t npass = (nrows + 64 / lpr - 1) / (64 / lpr);
-    const unsigned gx = (unsigned)((std::min<int64_t>(npass, per_expert) + GEMV_WAVES - 1) / GEMV_WAVES);
-    switch (lpr) {
-    case 8: launch(std::integral_constant<int, 8>(), gx); break;
-    case 16: launch(std::integral_constant<int, 16>(), gx); break;
-    case 32: launch(std::integral_constant<int, 32>(), gx); break;
-    default: launch(std::integral_constant<int, 64>(), gx); break;
+// Columns per pass for an expert kernel: an expert takes at most one slot per token when a token's ids
+// are distinct (top-k routing), so T tokens need at most T columns; repeated ids take more passes.
+static int expert_ncm(int64_t ntok) { return ntok <= 1 ? 1 : ntok == 2 ? 2 : ntok <= 4 ? 4 : 8; }
+
+// Launches an expert kernel: kptr(lpr, ncm) is the kernel for those template values (for its occupancy),
+// launch(lpr, ncm, gx) launches it. grid.x shares the GPU's wave slots among the expected routed
+// experts (uniform routing of n_slots slots) times `mats` matrices per expert. Few tokens: the slots
+// the kernel can hold at once, so every workgroup is resident and the short per-expert dependency
+// chain (ids, activations, weights) is paid once. Many tokens (8 and more): 8 waves per SIMD, which
+// oversubscribes the GPU; the longer per-wave streams then keep more loads in flight (measured).
+template <class KPtr, class Launch>
+static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int64_t n_slots, int64_t ntok, int mats,
+                                       KPtr kptr, Launch launch) {
+    auto with_ncm = [&](auto ncm) -> hipError_t {
+        const size_t lds = expert_lds(nb);
+        const int64_t slots =
+            (int64_t)device_cu_count() *
+            (ntok >= 8 ? 32 : resident_waves_per_cu(kptr(std::integral_constant<int, 16>(), ncm), GEMV_WAVES * 64, lds));
+        const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / (mats * expected_experts(n_expert, n_slots)));
+        const int lpr = gemv_lanes_per_row(nb, nrows, per_expert);
+        const int64_t npass = (nrows + 64 / lpr - 1) / (64 / lpr);
+        const unsigned gx = (unsigned)((std::min<int64_t>(npass, per_expert) + GEMV_WAVES - 1) / GEMV_WAVES);
+        switch (lpr) {
+        case 8: launch(std::integral_constant<int, 8>(), ncm, gx); break;
+        case 16: launch(std::integral_constant<int, 16>(), ncm, gx); break;
+        case 32: launch(std::integral_constant<int, 32>(), ncm, gx); break;
+        default: launch(std::integral_constant<int, 64>(), ncm, gx); break;
+        }
+        return hipGetLastError();
+    };
+    switch (expert_ncm(ntok)) {
+    case 1: return with_ncm(std::integral_constant<int, 1>());
+    case 2: return with_ncm(std::integral_constant<int, 2>());
+    case 4: return with_ncm(std::integral_constant<int, 4>());
+    default: return with_ncm(std::integral_constant<int, 8>());
     }
-    return hipGetLastError();
 }
 
 template <int F>
 static hipError_t launch_small(const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
                                hipStream_t stream) {
     const int64_t n_slots = (int64_t)a.n_used * a.ntok;
-    return launch_expert_kernel<F>(a.nb, a.nrows, a.n_expert, n_slots, 1, [&](auto lpr, unsigned gx) {
-        k_mmid_small<F, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(a.nb), stream>>>(
-            a, b, b_s1, b_s2, b_vec);
-    });
+    return launch_expert_kernel(
+        a.nb, a.nrows, a.n_expert, n_slots, a.ntok, 1,
+        [](auto lpr, auto ncm) { return (const void *)k_mmid_small<F, decltype(lpr)::value, decltype(ncm)::value>; },
+        [&](auto lpr, auto ncm, unsigned gx) {
+            k_mmid_small<F, decltype(lpr)::value, decltype(ncm)::value>
+                <<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(a.nb), stream>>>(a, b, b_s1, b_s2, b_vec);
+        });
 }
 
 hipError_t launch_mul_mat_id_small(int type, const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,
@@ -371,27 +401,31 @@ template <int FG, int FU, int FD>
 static hipError_t launch_moe_t(const MoeArgs &m, hipStream_t stream) {
     const int64_t n_slots = (int64_t)m.n_used * m.ntok;
     const int nb_in = m.n_embd / QK, nb_ff = m.n_ff / QK;
+    auto gate_up = [&](auto fmt, unsigned gz, int z0) {
+        constexpr int FZ = decltype(fmt)::value;
+        return launch_expert_kernel(
+            nb_in, m.n_ff, m.n_expert, n_slots, m.ntok, 2,
+            [](auto lpr, auto ncm) { return (const void *)k_moe_gate_up<FZ, decltype(lpr)::value, decltype(ncm)::value>; },
+            [&](auto lpr, auto ncm, unsigned gx) {
+                k_moe_gate_up<FZ, decltype(lpr)::value, decltype(ncm)::value>
+                    <<<dim3(gx, (unsigned)n_slots, gz), GEMV_WAVES * 64, expert_lds(nb_in), stream>>>(m, z0);
+            });
+    };
     hipError_t e;
     if (FG == FU) {
-        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
-            k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 2), GEMV_WAVES * 64,
-                                                       expert_lds(nb_in), stream>>>(m, 0);
-        });
+        e = gate_up(std::integral_constant<int, FG>(), 2, 0);
     } else {
-        e = launch_expert_kernel<FG>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
-            k_moe_gate_up<FG, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
-                                                       expert_lds(nb_in), stream>>>(m, 0);
-        });
-        if (e == hipSuccess)
-            e = launch_expert_kernel<FU>(nb_in, m.n_ff, m.n_expert, n_slots, 2, [&](auto lpr, unsigned gx) {
-                k_moe_gate_up<FU, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots, 1), GEMV_WAVES * 64,
-                                                           expert_lds(nb_in), stream>>>(m, 1);
-            });
+        e = gate_up(std::integral_constant<int, FG>(), 1, 0);
+        if (e == hipSuccess) e = gate_up(std::integral_constant<int, FU>(), 1, 1);
     }
     if (e != hipSuccess) return e;
-    return launch_expert_kernel<FD>(nb_ff, m.n_embd, m.n_expert, n_slots, 1, [&](auto lpr, unsigned gx) {
-        k_moe_down<FD, decltype(lpr)::value><<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(nb_ff), stream>>>(m);
-    });
+    return launch_expert_kernel(
+        nb_ff, m.n_embd, m.n_expert, n_slots, m.ntok, 1,
+        [](auto lpr, auto ncm) { return (const void *)k_moe_down<FD, decltype(lpr)::value, decltype(ncm)::value>; },
+        [&](auto lpr, auto ncm, unsigned gx) {
+            k_moe_down<FD, decltype(lpr)::value, decltype(ncm)::value>
+                <<<dim3(gx, (unsigned)n_slots), GEMV_WAVES * 64, expert_lds(nb_ff), stream>>>(m);
+        });
 }
 
 template <int FG, int FU>
@@ -414,13 +448,14 @@ static hipError_t launch_fmt(const MmidArgs &a, hipStream_t stream) {
     // grid rows: every possibly routed expert; grid columns sized for the expected number of distinct
     // experts under uniform routing, so the resident wave slots are shared among them
     const double expect = a.n_expert * (1.0 - std::pow(1.0 - 1.0 / a.n_expert, (double)n_slots));
-    const int64_t slots = (int64_t)device_cu_count() * 32;
+    const size_t lds = (size_t)MMID_NC * a.nb * gemv_lds_per_col_block() + MMID_NC * sizeof(int64_t);
+    const int64_t slots =
+        (int64_t)device_cu_count() * resident_waves_per_cu((const void *)k_mmid_gemv<F, 16>, GEMV_WAVES * 64, lds);
     const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, (int64_t)(slots / std::max(1.0, expect)));
     const int lpr = gemv_lanes_per_row(a.nb, a.nrows, per_expert);
     const int64_t npass = (a.nrows + 64 / lpr - 1) / (64 / lpr);
     const int64_t waves = std::min<int64_t>(npass, per_expert);
     const dim3 grid((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)max_active);
-    const size_t lds = (size_t)MMID_NC * a.nb * gemv_lds_per_col_block() + MMID_NC * sizeof(int64_t);
     switch (lpr) {
     case 8: k_mmid_gemv<F, 8><<<grid, GEMV_WAVES * 64, lds, stream>>>(a); break;
     case 16: k_mmid_gemv<F, 16><<<grid, GEMV_WAVES * 64, lds, stream>>>(a); break;

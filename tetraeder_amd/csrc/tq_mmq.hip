@@ -375,8 +375,7 @@ static hipError_t launch_cfg(const MmqArgs &a, hipStream_t stream) {
 
 template <int F>
 static hipError_t launch_fmt(const MmqArgs &a, hipStream_t stream) {
-    if (a.ncols <= 32) return launch_cfg<F, 1, 4, 1, 1>(a, stream);   // 32 x 128 tiles
-    if (a.ncols <= 64) return launch_cfg<F, 1, 4, 2, 1>(a, stream);   // 64 x 128
+    if (a.ncols <= 64) return launch_cfg<F, 1, 4, 2, 1>(a, stream);   // 64 x 128 tiles
     if (a.ncols <= 128) return launch_cfg<F, 2, 2, 2, 1>(a, stream);  // 128 x 64
     return launch_cfg<F, 4, 2, 2, 1>(a, stream);                       // 256 x 64, 8 waves
 }
