@@ -43,6 +43,16 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
     return __builtin_amdgcn_alignbyte(hi, lo, shift);
 }
 
+// Streaming loads of weight bytes that are read once: the non-temporal hint (global_load ... nt) keeps
+// them from displacing reused lines in L2 and the MALL; on MI355X a pure read stream reaches about
+// 7.3 TB/s with it against about 6.4 TB/s without.
+__device__ __forceinline__ uint32_t ld_stream(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint4 ld_stream4(const uint8_t *p) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load((const v4u *)p);
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
 __device__ __forceinline__ int sext8(uint32_t v, int bit) { return (int)(v << (24 - bit)) >> 24; }
 
 // v_bfi_b32: (a & mask) | (b & ~mask) in one instruction (the compiler splits the expression in two).

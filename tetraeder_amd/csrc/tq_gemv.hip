@@ -40,27 +40,41 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
                           });
 }
 
-// Lanes per row: fewer lanes per row amortize the cross-lane row sum over more super-blocks, as long as
-// there are enough row passes to keep every wave slot of the GPU busy (8 waves per SIMD).
-int gemv_lanes_per_row(int nb, int64_t nrows, int64_t slots) {
-    int lpr = 8, lpr_max = 8;
-    while (lpr_max < 64 && lpr_max < 8 * nb) lpr_max *= 2;  // no more super-block groups than blocks
-    while (lpr < lpr_max && (lpr < 8 * std::min(nb, 2) || (nrows + 64 / lpr - 1) / (64 / lpr) < slots)) lpr *= 2;
-    return lpr;
+// Lanes per row (a power of two from 4 to 64, at least nc: lanes 0 .. nc-1 of a row store its column
+// totals): a row's super-blocks are spread over LPR / 4 lane groups, and the most lanes per row that
+// leave no group idle are taken, so one wave load instruction covers 64 / LPR whole rows: a contiguous
+// byte range, the access pattern HBM streams best (on MI355X the Q6_K head ran 47.8 us with 8 lanes
+// per row and 45.8 us with whole rows per instruction).
+int gemv_lanes_per_row(int nb, int nc) {
+    int best = 0, best_idle = 1 << 30;
+    for (int lpr = 4; lpr <= 64; lpr *= 2) {
+        if (lpr < nc) continue;
+        const int g = lpr / LPB;
+        if (g > nb && best) break;
+        const int idle = g * ((nb + g - 1) / g) - nb;
+        if (idle <= best_idle) best = lpr, best_idle = idle;
+    }
+    return best;
 }
+
+// Waves a streaming GEMV launch uses: one workgroup of GEMV_WAVES per CU. More waves per CU made the
+// weight stream slower on MI355X (the head GEMV: 45.8 us at 8 waves per CU, 54.4 us at 16, 64.4 us
+// at 12 with the extra workgroups on a third of the CUs), because the extra in-flight loads only
+// contend for the CU's memory pipeline once every HBM channel is busy.
+int64_t gemv_stream_waves() { return (int64_t)device_cu_count() * GEMV_WAVES; }
 
 template <int F, int NC>
 static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
     const size_t lds = (size_t)NC * a.nb * gemv_lds_per_col_block();
-    // resident wave slots of the GPU for this kernel (registers and LDS permitting)
-    const int64_t slots = (int64_t)device_cu_count() * resident_waves_per_cu((const void *)k_gemv<F, NC, 16>,
-                                                                              GEMV_WAVES * 64, lds);
-    const int lpr = gemv_lanes_per_row(a.nb, a.nrows, slots);
+    const int lpr = gemv_lanes_per_row(a.nb, NC);
     const int rpw = 64 / lpr;
     const int64_t npass = (a.nrows + rpw - 1) / rpw;
-    const int64_t waves = std::min<int64_t>(npass, slots);
+    const int64_t waves = std::min<int64_t>(npass, gemv_stream_waves());
     const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
     switch (lpr) {
+    case 4:
+        if constexpr (NC <= 4) k_gemv<F, NC, 4><<<g2, GEMV_WAVES * 64, lds, stream>>>(a);
+        break;
     case 8: k_gemv<F, NC, 8><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
     case 16: k_gemv<F, NC, 16><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;
     case 32: k_gemv<F, NC, 32><<<g2, GEMV_WAVES * 64, lds, stream>>>(a); break;

@@ -2,13 +2,15 @@
 // Q8_K activation staging in LDS and the per-wave row stream over Q4_K / Q6_K super-blocks.
 //
 // Layout of the work (the path is HBM-bound: every weight byte is read once and used ncols times):
-//   - a workgroup stages its Q8_K activation columns in LDS once, re-ordered so each lane reads the 32
-//     activation bytes that pair with its weights as two 16-byte LDS reads;
-//   - each wave streams rows: LPR lanes per row (8 lanes per super-block, LPR/8 super-blocks of a row in
+//   - a workgroup stages its Q8_K activation columns in LDS once, re-ordered so each lane reads the 64
+//     activation bytes that pair with its weights as four 16-byte LDS reads;
+//   - each wave streams rows: LPR lanes per row (4 lanes per super-block, LPR/4 super-blocks of a row in
 //     flight), 64/LPR rows per wave pass, passes interleaved over the waves of the matrix;
-//   - a lane covers 32 weights of a super-block: Q4_K one 16-byte load of qs plus the 16-byte header,
-//     Q6_K three 8-byte windows (ql, ql+32, qh) and the scale/d tail, read as the 4-byte-aligned dwords
-//     that contain the window and re-aligned with v_alignbyte (a Q6_K block is only 2-byte aligned);
+//   - a lane covers 64 weights of a super-block, so the per-item work (addressing, realignment, scale
+//     unpack, the fp32 combination) is spread over twice the bytes of a 32-weight split: Q4_K the
+//     16-byte header and two 16-byte qs words, Q6_K three 16-byte windows (ql, ql+32, qh) and the
+//     scale/d tail, read as the 4-byte-aligned dwords that contain each window and re-aligned with
+//     v_alignbyte (a Q6_K block is only 2-byte aligned);
 //   - integer sub-block sums with v_dot4_i32_i8, the Q4_K mins and the Q6_K -32 offset folded in
 //     through the Q8_K bsums (the iqk scheme, patches/0002-iqk-avx512-q4k-q6k-decode.patch:1296-1342,
 //     1638-1663, 1713-1722), one fp32 multiply-add per super-block and column;
@@ -24,24 +26,28 @@ namespace tq {
 constexpr int GEMV_WAVES = 8;
 constexpr int ACT_BS_BYTES = 64;  // per (column, block): 8 lanes x up to 4 int16 bsums
 
-// Where lane u's activation bytes live: 32 bytes per lane, in the order the lane consumes them.
-// Q4_K lane u = 2c + half: [y[64c + 16half + 0..15] | y[64c + 32 + 16half + 0..15]].
-// Q6_K lane u = 4h + v:    [y[128h + 32k + 8v + 0..7] for k = 0..3].
+constexpr int LPB = 4;  // lanes per super-block
+
+// Where lane u's activation bytes live: 64 bytes per lane, in the order the lane consumes them.
+// Q4_K lane u: y[64u .. 64u+63] in order (qs[32u .. 32u+31] low nibbles pair with the first 32, high
+//   nibbles with the last 32), so the layout is the identity.
+// Q6_K lane u = 2h + v: [y[128h + 32k + 16v + 0..15] for k = 0..3].
 template <int F> __device__ __forceinline__ int act_perm(int e) {
     if (F == FMT_Q4K) {
-        const int c = e >> 6, r = e & 63, part = r >> 5, l = r & 31, half = l >> 4, off = l & 15;
-        return (2 * c + half) * 32 + part * 16 + off;
+        return e;
     } else {
-        const int h = e >> 7, r = e & 127, k = r >> 5, l = r & 31, v = l >> 3, j = l & 7;
-        return (4 * h + v) * 32 + 8 * k + j;
+        const int h = e >> 7, r = e & 127, k = r >> 5, l = r & 31, v = l >> 4, j = l & 15;
+        return (2 * h + v) * 64 + 16 * k + j;
     }
 }
 
-// bsums slot s of lane u: Q4_K two slots (the lane's 16-element halves of sub-blocks 2c and 2c+1),
-// Q6_K four slots (the 16-element groups its four 8-element windows belong to).
+// bsums slots of lane u (int16 each, ACT_SLOTS per lane): Q4_K two 32-element sums (sub-blocks 2u and
+// 2u+1, each the sum of two Q8_K bsums); Q6_K the four 16-element bsums of its groups 8h + 2k + v.
+template <int F> struct ActSlots { static constexpr int n = F == FMT_Q4K ? 2 : 4; };
+// The Q8_K 16-element bsums index of slot s of lane u (Q6_K), or the first of the two summed (Q4_K).
 template <int F> __device__ __forceinline__ int act_bs_src(int u, int s) {
-    if (F == FMT_Q4K) return 4 * (u >> 1) + (u & 1) + 2 * s;
-    return 8 * (u >> 2) + 2 * s + ((u & 3) >> 1);
+    if (F == FMT_Q4K) return 4 * u + 2 * s;
+    return 8 * (u >> 1) + 2 * s + (u & 1);
 }
 
 // Stages NC Q8_K activation columns (column c of nb blocks starting at col_src(c), c < ncols; zeros
@@ -57,13 +63,17 @@ __device__ __forceinline__ void stage_activations(ColSrc col_src, int nb, int nc
         if (c < ncols) v = *(const uint32_t *)(col_src(c) + (size_t)b * Q8K_BYTES + Q8K_QS + 4 * t);
         *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * t)) = v;
     }
-    constexpr int SLOTS = F == FMT_Q4K ? 2 : 4;
-    const int nbs = NC * nb * 8 * SLOTS;
+    constexpr int SLOTS = ActSlots<F>::n;
+    const int nbs = NC * nb * LPB * SLOTS;
     for (int i = tid; i < nbs; i += nthr) {
-        const int s = i % SLOTS, u = (i / SLOTS) & 7, cb = i / (SLOTS * 8), c = cb / nb, b = cb - c * nb;
-        int16_t v = 0;
-        if (c < ncols) v = *(const int16_t *)(col_src(c) + (size_t)b * Q8K_BYTES + Q8K_BSUMS + 2 * act_bs_src<F>(u, s));
-        lds_bs[cb * (ACT_BS_BYTES / 2) + u * SLOTS + s] = v;
+        const int s = i % SLOTS, u = (i / SLOTS) % LPB, cb = i / (SLOTS * LPB), c = cb / nb, b = cb - c * nb;
+        int v = 0;
+        if (c < ncols) {
+            const int16_t *bs = (const int16_t *)(col_src(c) + (size_t)b * Q8K_BYTES + Q8K_BSUMS);
+            const int g = act_bs_src<F>(u, s);
+            v = F == FMT_Q4K ? bs[g] + bs[g + 1] : bs[g];
+        }
+        lds_bs[cb * (ACT_BS_BYTES / 2) + u * SLOTS + s] = (int16_t)v;
     }
     for (int i = tid; i < NC * nb; i += nthr) {
         const int c = i / nb, b = i - c * nb;
@@ -108,12 +118,13 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
     }
     *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * lane)) = packed;
     sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);  // lanes 4g..4g+3 hold the sum of group g
-    constexpr int SLOTS = F == FMT_Q4K ? 2 : 4;
-    const int slot = lane < 8 * SLOTS ? lane : 0;
+    sum += __shfl_xor(sum, 2, 64);  // lanes 4g..4g+3 hold the sum of 16-element group g
+    if (F == FMT_Q4K) sum += __shfl_xor(sum, 4, 64);  // lanes 8g..8g+7: the 32-element sum of 2g, 2g+1
+    constexpr int SLOTS = ActSlots<F>::n;
+    const int slot = lane < LPB * SLOTS ? lane : 0;
     const int g = act_bs_src<F>(slot / SLOTS, slot % SLOTS);
     const int bs = __shfl(sum, 4 * g, 64);
-    if (lane < 8 * SLOTS) lds_bs[cb * (ACT_BS_BYTES / 2) + lane] = (int16_t)bs;
+    if (lane < LPB * SLOTS) lds_bs[cb * (ACT_BS_BYTES / 2) + lane] = (int16_t)bs;
     if (lane == 0) lds_d[cb] = d;
 }
 
@@ -157,69 +168,76 @@ template <int NC> struct Acc {
 // next item's loads are in flight while the current item is computed.
 template <int F> struct Item;
 
-// Q4_K lane u = 2c + half covers qs[16u .. 16u+15]: the 16-byte header and one 16-byte qs word.
+// Q4_K lane u covers qs[32u .. 32u+31] (elements 64u .. 64u+63, sub-blocks 2u and 2u+1): the 16-byte
+// header and two 16-byte qs words.
 template <> struct Item<FMT_Q4K> {
-    uint4 hdr, qv;
+    uint4 hdr, q0, q1;
     bool valid;
     __device__ __forceinline__ void load(const uint8_t *__restrict__ w, uint32_t off, int u) {
         hdr = *(const uint4 *)(w + off);
-        qv = *(const uint4 *)(w + (off + 16 + 16 * u));
+        q0 = *(const uint4 *)(w + (off + 16 + 32 * u));
+        q1 = *(const uint4 *)(w + (off + 32 + 32 * u));
     }
 };
 
-// Q6_K lane u = 4h + v covers elements 128h + 32k + 8v + 0..7, k = 0..3: 8-byte windows of ql at
-// 64h+8v and 64h+32+8v and of qh at 128+32h+8v, plus the scale/d tail at 192..209. A block starts
-// at an even address; every window is read as the aligned dwords that contain it (3 dwords per
+// Q6_K lane u = 2h + v covers elements 128h + 32k + 16v + 0..15, k = 0..3: 16-byte windows of ql at
+// 64h+16v and 64h+32+16v and of qh at 128+32h+16v, plus the scale/d tail at 192..209. A block starts
+// at an even address; every window is read as the aligned dwords that contain it (5 dwords per
 // window, 5 for the tail) and realigned by sh bytes.
 template <> struct Item<FMT_Q6K> {
-    uint32_t a0, a1, a2, b0, b1, b2, h0, h1, h2, t0, t1, t2, t3, t4, sh;
+    uint32_t a[5], b[5], q[5], t[5], sh;
     bool valid;
     // w is 4-byte aligned (checked by the host); off is the block's byte offset, even.
     __device__ __forceinline__ void load(const uint8_t *__restrict__ w, uint32_t off, int u) {
-        const uint32_t h = (uint32_t)u >> 2, v = (uint32_t)u & 3;
+        const uint32_t h = (uint32_t)u >> 1, v = (uint32_t)u & 1;
         sh = off & 3u;
         const uint32_t o0 = off - sh;  // 4-byte aligned
-        const uint32_t *pa = (const uint32_t *)(w + (o0 + 64 * h + 8 * v));
-        const uint32_t *pb = (const uint32_t *)(w + (o0 + 64 * h + 32 + 8 * v));
-        const uint32_t *ph = (const uint32_t *)(w + (o0 + 128 + 32 * h + 8 * v));
+        const uint32_t *pa = (const uint32_t *)(w + (o0 + 64 * h + 16 * v));
+        const uint32_t *pb = (const uint32_t *)(w + (o0 + 64 * h + 32 + 16 * v));
+        const uint32_t *ph = (const uint32_t *)(w + (o0 + 128 + 32 * h + 16 * v));
         const uint32_t *pt = (const uint32_t *)(w + (o0 + 192));
-        a0 = pa[0], a1 = pa[1], a2 = pa[2];
-        b0 = pb[0], b1 = pb[1], b2 = pb[2];
-        h0 = ph[0], h1 = ph[1], h2 = ph[2];
-        t0 = pt[0], t1 = pt[1], t2 = pt[2], t3 = pt[3], t4 = pt[4];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) a[i] = pa[i], b[i] = pb[i], q[i] = ph[i], t[i] = pt[i];
     }
 };
 
 template <int NC>
 __device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
                                              const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
-    const uint4 hdr = it.hdr, qv = it.qv;
+    const uint4 hdr = it.hdr;
     // an invalid item read a valid stand-in block; zero scales make its contribution exactly 0
     const float d = it.valid ? half_bits_to_float(hdr.x) : 0.f;
     const float dmin = it.valid ? half_bits_to_float(hdr.x >> 16) : 0.f;
-    const int c = u >> 1;
+    // 6-bit scales and mins of sub-blocks 2u and 2u+1 (ggml's get_scale_min_k4)
     uint32_t scw, mw;
-    if (c < 2) {
+    if (u < 2) {
         scw = hdr.y & 0x3f3f3f3fu;
         mw = hdr.z & 0x3f3f3f3fu;
     } else {
         scw = (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u);
         mw = ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u);
     }
-    const int sh = (c & 1) * 16;
+    const int sh = (u & 1) * 16;
     const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
     const int m_lo = (mw >> sh) & 0xff, m_hi = (mw >> (sh + 8)) & 0xff;
-    const uint32_t lo0 = qv.x & 0x0f0f0f0fu, lo1 = qv.y & 0x0f0f0f0fu, lo2 = qv.z & 0x0f0f0f0fu,
-                   lo3 = qv.w & 0x0f0f0f0fu;
-    const uint32_t hi0 = (qv.x >> 4) & 0x0f0f0f0fu, hi1 = (qv.y >> 4) & 0x0f0f0f0fu,
-                   hi2 = (qv.z >> 4) & 0x0f0f0f0fu, hi3 = (qv.w >> 4) & 0x0f0f0f0fu;
+    const uint32_t qw[8] = {it.q0.x, it.q0.y, it.q0.z, it.q0.w, it.q1.x, it.q1.y, it.q1.z, it.q1.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) lo[i] = qw[i] & 0x0f0f0f0fu, hi[i] = (qw[i] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
         const int cb = cb0 + col * nb;
-        const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
-        const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
-        const int slo = dot4(lo3, y0.w, dot4(lo2, y0.z, dot4(lo1, y0.y, dot4(lo0, y0.x, 0))));
-        const int shi = dot4(hi3, y1.w, dot4(hi2, y1.z, dot4(hi1, y1.y, dot4(hi0, y1.x, 0))));
+        const uint8_t *y = lds_qs + cb * 256 + u * 64;
+        const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
+        const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
+        int slo = dot4(lo[0], y0.x, 0);
+        slo = dot4(lo[1], y0.y, slo), slo = dot4(lo[2], y0.z, slo), slo = dot4(lo[3], y0.w, slo);
+        slo = dot4(lo[4], y1.x, slo), slo = dot4(lo[5], y1.y, slo), slo = dot4(lo[6], y1.z, slo);
+        slo = dot4(lo[7], y1.w, slo);
+        int shi = dot4(hi[0], y2.x, 0);
+        shi = dot4(hi[1], y2.y, shi), shi = dot4(hi[2], y2.z, shi), shi = dot4(hi[3], y2.w, shi);
+        shi = dot4(hi[4], y3.x, shi), shi = dot4(hi[5], y3.y, shi), shi = dot4(hi[6], y3.z, shi);
+        shi = dot4(hi[7], y3.w, shi);
         const uint32_t bsw = *(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2);
         const int isum = mad24(sc_lo, slo, mul24(sc_hi, shi));
         const int msum = mad24(m_lo, (int)(int16_t)(bsw & 0xffffu), mul24(m_hi, (int)(int16_t)(bsw >> 16)));
@@ -230,43 +248,50 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int
 template <int NC>
 __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
                                              const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
-    const int h = u >> 2, v = u & 3;
+    const int h = u >> 1, v = u & 1;
     const uint32_t sh = it.sh;
-    const uint32_t A0 = align_bytes(it.a1, it.a0, sh), A1 = align_bytes(it.a2, it.a1, sh);
-    const uint32_t B0 = align_bytes(it.b1, it.b0, sh), B1 = align_bytes(it.b2, it.b1, sh);
-    const uint32_t H0 = align_bytes(it.h1, it.h0, sh), H1 = align_bytes(it.h2, it.h1, sh);
-    // scales[4j .. 4j+3] for j = 2h and 2h+1 (this lane's four scales live there)
-    const uint32_t s01 = h ? align_bytes(it.t3, it.t2, sh) : align_bytes(it.t1, it.t0, sh);
-    const uint32_t s23 = h ? align_bytes(it.t4, it.t3, sh) : align_bytes(it.t2, it.t1, sh);
-    const float d = it.valid ? half_bits_to_float(it.t4 >> (8 * sh)) : 0.f;
-    const int pos = 8 * (v >> 1);
+    uint32_t A[4], B[4], H[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        A[i] = align_bytes(it.a[i + 1], it.a[i], sh);
+        B[i] = align_bytes(it.b[i + 1], it.b[i], sh);
+        H[i] = align_bytes(it.q[i + 1], it.q[i], sh);
+    }
+    // scales[8h .. 8h+7] (this lane's four scales, bytes v, v+2, v+4, v+6 of them) and d
+    const uint32_t s01 = h ? align_bytes(it.t[3], it.t[2], sh) : align_bytes(it.t[1], it.t[0], sh);
+    const uint32_t s23 = h ? align_bytes(it.t[4], it.t[3], sh) : align_bytes(it.t[2], it.t[1], sh);
+    const float d = it.valid ? half_bits_to_float(it.t[4] >> (8 * sh)) : 0.f;
+    const int pos = 8 * v;
     const int sc0 = sext8(s01, pos), sc1 = sext8(s01, pos + 16), sc2 = sext8(s23, pos), sc3 = sext8(s23, pos + 16);
-    // 6-bit codes: low nibble from ql, bits 4-5 from the qh field of the quarter. Hl keeps qh bits
-    // (0,1) and (4,5) of every byte, Hh bits (2,3) and (6,7) moved down by two; a bit-field insert then
-    // merges nibble and high bits without the neighbour byte's bits leaking in.
+    // 6-bit codes of quarter k: low nibble from ql (k = 0, 1 low nibbles of A, B; k = 2, 3 high nibbles),
+    // bits 4-5 from the qh field of the quarter. Hl keeps qh bits (0,1) and (4,5) of every byte, Hh bits
+    // (2,3) and (6,7) moved down by two; a bit-field insert merges nibble and high bits without the
+    // neighbour byte's bits leaking in.
     const uint32_t m4 = 0x0f0f0f0fu;
-    const uint32_t Hl0 = H0 & 0x33333333u, Hl1 = H1 & 0x33333333u;
-    const uint32_t Hh0 = (H0 >> 2) & 0x33333333u, Hh1 = (H1 >> 2) & 0x33333333u;
-    const uint32_t q00 = bfi(m4, A0, Hl0 << 4), q01 = bfi(m4, A1, Hl1 << 4);
-    const uint32_t q10 = bfi(m4, B0, Hh0 << 4), q11 = bfi(m4, B1, Hh1 << 4);
-    const uint32_t q20 = bfi(m4, A0 >> 4, Hl0), q21 = bfi(m4, A1 >> 4, Hl1);
-    const uint32_t q30 = bfi(m4, B0 >> 4, Hh0), q31 = bfi(m4, B1 >> 4, Hh1);
-    // the -32 offset enters once per 16-element group, on the even lane of the pair sharing it
-    const int even = (v & 1) ? 0 : -32;
+    uint32_t c0[4], c1[4], c2[4], c3[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t Hl = H[i] & 0x33333333u, Hh = (H[i] >> 2) & 0x33333333u;
+        c0[i] = bfi(m4, A[i], Hl << 4);
+        c1[i] = bfi(m4, B[i], Hh << 4);
+        c2[i] = bfi(m4, A[i] >> 4, Hl);
+        c3[i] = bfi(m4, B[i] >> 4, Hh);
+    }
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
         const int cb = cb0 + col * nb;
-        const uint4 y0 = *(const uint4 *)(lds_qs + cb * 256 + u * 32);
-        const uint4 y1 = *(const uint4 *)(lds_qs + cb * 256 + u * 32 + 16);
-        const int S0 = dot4(q01, y0.y, dot4(q00, y0.x, 0));
-        const int S1 = dot4(q11, y0.w, dot4(q10, y0.z, 0));
-        const int S2 = dot4(q21, y1.y, dot4(q20, y1.x, 0));
-        const int S3 = dot4(q31, y1.w, dot4(q30, y1.z, 0));
+        const uint8_t *y = lds_qs + cb * 256 + u * 64;
+        const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
+        const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
+        const int S0 = dot4(c0[3], y0.w, dot4(c0[2], y0.z, dot4(c0[1], y0.y, dot4(c0[0], y0.x, 0))));
+        const int S1 = dot4(c1[3], y1.w, dot4(c1[2], y1.z, dot4(c1[1], y1.y, dot4(c1[0], y1.x, 0))));
+        const int S2 = dot4(c2[3], y2.w, dot4(c2[2], y2.z, dot4(c2[1], y2.y, dot4(c2[0], y2.x, 0))));
+        const int S3 = dot4(c3[3], y3.w, dot4(c3[2], y3.z, dot4(c3[1], y3.y, dot4(c3[0], y3.x, 0))));
         const uint2 bsw = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
         const int corr = mad24(sc0, (int)(int16_t)(bsw.x & 0xffffu),
                                mad24(sc1, (int)(int16_t)(bsw.x >> 16),
                                      mad24(sc2, (int)(int16_t)(bsw.y & 0xffffu), mul24(sc3, (int)(int16_t)(bsw.y >> 16)))));
-        const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mad24(sc3, S3, mul24(even, corr)))));
+        const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mad24(sc3, S3, mul24(-32, corr)))));
         acc.v[col] += (lds_d[cb] * d) * (float)isum;
     }
 }
@@ -281,10 +306,11 @@ template <int F, int NC, int LPR, class Stage, class Store>
 __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nrows, int nb, uint32_t row_stride, int wave,
                                           int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs, const float *lds_d,
                                           Stage stage, Store store) {
-    constexpr int G = LPR / 8;     // super-blocks of a row in flight per wave pass
+    static_assert(LPR >= LPB && LPR <= 64, "lanes per row");
+    constexpr int G = LPR / LPB;   // super-blocks of a row in flight per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     const int lane = lane_id();
-    const int u = lane & 7, gb = (lane % LPR) >> 3, lrow = lane / LPR, lir = lane % LPR;
+    const int u = lane % LPB, gb = (lane % LPR) / LPB, lrow = lane / LPR, lir = lane % LPR;
     const int npass = (nrows + RPW - 1) / RPW;
     const bool active = wave < npass;  // uniform over the wave
 

@@ -58,8 +58,9 @@ hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }
 
-// Lanes per weight row for an nrows x (nb super-blocks) matrix when `slots` waves can be resident.
-int gemv_lanes_per_row(int nb, int64_t nrows, int64_t slots);
+// Lanes per weight row of a streaming GEMV over rows of nb super-blocks, and the waves a launch uses.
+int gemv_lanes_per_row(int nb, int nc);
+int64_t gemv_stream_waves();
 
 // MUL_MAT_ID over Q8_K activations: routing on the device, then one expert GEMV per routed expert.
 struct MmidArgs {

@@ -359,10 +359,13 @@ static hipError_t launch_expert_kernel(int nb, int64_t nrows, int n_expert, int6
             (int64_t)device_cu_count() *
             (ntok >= 8 ? 32 : resident_waves_per_cu(kptr(std::integral_constant<int, 16>(), ncm), GEMV_WAVES * 64, lds));
         const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, slots / (mats * expected_experts(n_expert, n_slots)));
-        const int lpr = gemv_lanes_per_row(nb, nrows, per_expert);
+        const int lpr = gemv_lanes_per_row(nb, decltype(ncm)::value);
         const int64_t npass = (nrows + 64 / lpr - 1) / (64 / lpr);
         const unsigned gx = (unsigned)((std::min<int64_t>(npass, per_expert) + GEMV_WAVES - 1) / GEMV_WAVES);
         switch (lpr) {
+        case 4:
+            if constexpr (decltype(ncm)::value <= 4) launch(std::integral_constant<int, 4>(), ncm, gx);
+            break;
         case 8: launch(std::integral_constant<int, 8>(), ncm, gx); break;
         case 16: launch(std::integral_constant<int, 16>(), ncm, gx); break;
         case 32: launch(std::integral_constant<int, 32>(), ncm, gx); break;
@@ -452,7 +455,7 @@ static hipError_t launch_fmt(const MmidArgs &a, hipStream_t stream) {
     const int64_t slots =
         (int64_t)device_cu_count() * resident_waves_per_cu((const void *)k_mmid_gemv<F, 16>, GEMV_WAVES * 64, lds);
     const int64_t per_expert = std::max<int64_t>(GEMV_WAVES, (int64_t)(slots / std::max(1.0, expect)));
-    const int lpr = gemv_lanes_per_row(a.nb, a.nrows, per_expert);
+    const int lpr = gemv_lanes_per_row(a.nb, MMID_NC);
     const int64_t npass = (a.nrows + 64 / lpr - 1) / (64 / lpr);
     const int64_t waves = std::min<int64_t>(npass, per_expert);
     const dim3 grid((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)max_active);
