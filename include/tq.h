@@ -128,6 +128,14 @@ int tq_moe_ffn(const tq_tensor *gate_exps, const tq_tensor *up_exps, const tq_te
                const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
                void *stream);
 
+/* Failed cross-workgroup waits of the single-launch MoE step (tq_moe_ffn up to 256 slots) on the current
+ * device since the last clear: *count gets the error word (0: none), clear != 0 resets it. The step's
+ * workgroups wait for each other with bounded polls; a wait that runs out (only possible when the GPU
+ * cannot hold all of the launch's workgroups at once) leaves that call's outputs undefined. Synchronous
+ * (reads device memory). No reference counterpart: ggml's CUDA MUL_MAT_ID runs its nodes as separate
+ * launches. */
+int tq_moe_ffn_sync_errors(unsigned *count, int clear);
+
 /* Dequantize n elements of type (Q4_K, Q6_K or Q8_K; n a multiple of 256) from src to F32 dst.
  * Replaces ggml_get_type_traits(ty)->to_float as used by quant::to_f32
  * (crates/ggml-sys/src/ggml/quant.rs:20-48) for device buffers. */

@@ -99,3 +99,33 @@ def test_moe_ffn_matches_composed_ops(gpu):
     ref = ggml.mul_mat_id(down, act, ids)
     worst = float((fused - ref).abs().max() / ref.abs().max())
     assert worst <= 1e-3, worst
+
+
+def test_moe_ffn_back_to_back_calls(gpu):
+    """Consecutive single-launch steps with changing token counts and ids, on one stream with no host
+    synchronization between them (as a decode loop issues them): each equals its own nodes run through
+    mul_mat_id, so the cross-workgroup progress counters start from zero on every call, and no wait
+    ran out."""
+    _case("back to back")
+    n_embd, n_ff, E = 2048, 768, 128
+    gate = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=31, device=gpu)
+    up = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=32, device=gpu)
+    down = make_experts(ggml.Type.Q6_K, n_ff, n_embd, E, seed=33, device=gpu)
+    ggml.moe_sync_errors(clear=True)
+    cases = []
+    for i, T in enumerate((1, 16, 3, 1, 32, 8, 2, 1)):
+        ids = torch.from_numpy(qwen3_moe_ids(T, seed=700 + i)).to(gpu)
+        x = torch.from_numpy(normal((T, 1, n_embd), 800 + i)).to(gpu)
+        w = torch.from_numpy(np.random.default_rng(i).random((T, 8, 1)).astype(np.float32)).to(gpu)
+        cases.append((ids, x, w, ggml.moe_ffn(gate, up, down, x, ids, w)))
+    torch.cuda.synchronize()
+    assert ggml.moe_sync_errors() == 0
+    for ids, x, w, fused in cases:
+        g = ggml.mul_mat_id(gate, x, ids)
+        u = ggml.mul_mat_id(up, x, ids)
+        act = (g / (1 + torch.exp(-g)) * u).contiguous()
+        ref = ggml.mul_mat_id(down, act, ids) * w
+        ref[ids < 0] = 0.0
+        assert bool((fused[ids < 0] == 0).all())
+        worst = float((fused - ref).abs().max() / ref.abs().max())
+        assert worst <= 3e-3, worst

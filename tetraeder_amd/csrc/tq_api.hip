@@ -445,6 +445,8 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
                      m.rw_s2 = (int64_t)(weights->nb[2] / 4);
         m.gu = gu;
         m.dst = (float *)dst->data, m.o_s1 = (int64_t)(dst->nb[1] / 4), m.o_s2 = (int64_t)(dst->nb[2] / 4);
+        if (moe_fused_supported(gate->type, up->type, m))
+            return check_hip(launch_moe_fused(gate->type, down->type, m, 0, s), "moe_ffn launch");
         return check_hip(launch_moe_ffn(gate->type, up->type, down->type, m, s), "moe_ffn launch");
     }
     // Many tokens: the same nodes composed, MUL_MAT_ID with device routing and elementwise glue.
@@ -466,6 +468,11 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
                                            (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4), s),
                          "scale_rows launch");
     return TQ_STATUS_SUCCESS;
+}
+
+int tq_moe_ffn_sync_errors(unsigned *count, int clear) {
+    if (!count) return fail(TQ_STATUS_FAILED, "NULL count");
+    return check_hip(moe_sync_errors(count, clear != 0), "moe sync error read");
 }
 
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {

@@ -296,17 +296,29 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
     }
 }
 
+// Item loads a lane keeps in flight while it computes: the lane walks its items through a ring of
+// GEMV_PF register sets, issuing item k + GEMV_PF - 1 before computing item k.
+#ifndef TQ_GEMV_PF
+#define TQ_GEMV_PF 3
+#endif
+constexpr int GEMV_PF = TQ_GEMV_PF;
+
 // Streams rows [0, nrows) of one weight matrix (nb super-blocks per row, row_stride bytes apart) against
 // the NC columns staged in LDS; this wave takes passes wave, wave + nwaves, ... of 64/LPR rows each.
 // store(c, row, value) receives every row total of column c (called by one lane per row and column).
 // stage() runs on every wave of the workgroup after the wave's first weight loads are issued and
 // before the first item is computed: it fills the LDS columns (and ends with a workgroup barrier), so
 // the activation staging overlaps the weights' memory latency.
-template <int F, int NC, int LPR, class Stage, class Store>
-__device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nrows, int nb, uint32_t row_stride, int wave,
-                                          int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs, const float *lds_d,
-                                          Stage stage, Store store) {
+// The stream over M matrices of the same shape and row stride at once (M = 1: plain GEMV; M = 2: the
+// MoE gate and up projections, whose rows meet in one store of both totals): a lane's item at
+// (pass, super-block) holds the blocks of every matrix at that position, and they share the
+// activation columns staged in LDS.
+template <int F, int NC, int LPR, int M, int PF, class Stage, class Store>
+__device__ __forceinline__ void gemv_rows_m(const uint8_t *const (&ws)[M], int nrows, int nb, uint32_t row_stride,
+                                            int wave, int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs,
+                                            const float *lds_d, Stage stage, Store store) {
     static_assert(LPR >= LPB && LPR <= 64, "lanes per row");
+    static_assert(PF >= 2, "prefetch ring");
     constexpr int G = LPR / LPB;   // super-blocks of a row in flight per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     const int lane = lane_id();
@@ -316,60 +328,106 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nro
 
     // Wave passes are interleaved over the matrix (pass wave, wave + nwaves, ...), so at any moment the
     // resident waves read one contiguous stretch of rows: HBM streams best that way. The lane walks
-    // items (pass p, j): row p*RPW + lrow, super-block gb + j*G, j < BPL. The next item's loads are
-    // issued before the current item is computed; the two item registers alternate (the loop body
-    // is unrolled twice) so nothing is copied. Weights are addressed by 32-bit byte offsets from the
-    // matrix base (the host keeps each matrix below 4 GiB).
+    // items (pass p, j): row p*RPW + lrow, super-block gb + j*G, j < BPL. Item k + PF - 1 is loaded
+    // before item k is computed; the ring of item registers is indexed by compile-time slots (the loop
+    // body is unrolled PF times) so nothing is copied. Weights are addressed by 32-bit byte offsets from
+    // the matrix base (the host keeps each matrix below 4 GiB).
     const int BPL = (nb + G - 1) / G;
     constexpr int BYTES = FmtInfo<F>::bytes;
     struct Pos {
         int p, j, row;
         uint32_t row_off;
     };
-    Pos cur{wave, 0, wave * RPW + lrow, 0};
-    cur.row_off = (uint32_t)cur.row * row_stride;
     const int nw = nwaves;
     const uint32_t pass_stride = (uint32_t)(nw * RPW) * row_stride;
-    // Loads are unconditional so the compiler can leave the next item's loads in flight: an item past
-    // the rows or blocks reads block 0 of the matrix instead and is masked by its valid flag.
-    auto load = [&](Item<F> &it, const Pos &q) {
+    auto advance = [&](Pos &q) {
+        if (++q.j == BPL) q.j = 0, q.p += nw, q.row += nw * RPW, q.row_off += pass_stride;
+    };
+    Pos cur{wave, 0, wave * RPW + lrow, 0};
+    cur.row_off = (uint32_t)cur.row * row_stride;
+    Pos ld = cur;
+    // Loads are unconditional so the compiler can leave them in flight: an item past the rows or blocks
+    // reads block 0 of the matrix instead and is masked by its valid flag.
+    auto load = [&](Item<F> (&it)[M], const Pos &q) {
         const int b = gb + q.j * G;
-        it.valid = q.row < nrows && b < nb;
-        it.load(w, it.valid ? q.row_off + (uint32_t)(b * BYTES) : 0u, u);
-    };
-    Acc<NC> acc;
+        const bool valid = q.row < nrows && b < nb;
+        const uint32_t off = valid ? q.row_off + (uint32_t)(b * BYTES) : 0u;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
-    // One step: issue the next item's loads into `nxt`, compute `now`, finish the row if it ends here.
-    auto step = [&](Item<F> &now, Item<F> &nxt) -> bool {
-        Pos n = cur;
-        if (++n.j == BPL) n.j = 0, n.p += nw, n.row += nw * RPW, n.row_off += pass_stride;
-        const bool more = n.p < npass;  // uniform over the wave
-        load(nxt, n);
-        const int b = min(gb + cur.j * G, nb - 1);  // LDS column block; an invalid item has zero scales
-        compute_item<NC>(now, u, b, nb, lds_qs, lds_bs, lds_d, acc);
-        if (cur.j == BPL - 1) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
-            if (cur.row < nrows) {
-#pragma unroll
-                for (int c = 0; c < NC; ++c)
-                    if (lir == c) store(c, cur.row, acc.v[c]);
-            }
-#pragma unroll
-            for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
+        for (int mi = 0; mi < M; ++mi) {
+            it[mi].valid = valid;
+            it[mi].load(ws[mi], off, u);
         }
-        cur = n;
-        return more;
     };
-    Item<F> A, B;
-    if (active) load(A, cur);
+    Acc<NC> acc[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[mi].v[c] = 0.f;
+    Item<F> ring[PF][M];
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < PF - 1; ++i) {
+            load(ring[i], ld);
+            advance(ld);
+        }
+    }
     stage();
     if (!active) return;
     for (;;) {
-        if (!step(A, B)) break;
-        if (!step(B, A)) break;
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            load(ring[(s + PF - 1) % PF], ld);
+            advance(ld);
+            const int b = min(gb + cur.j * G, nb - 1);  // LDS column block; an invalid item has zero scales
+#pragma unroll
+            for (int mi = 0; mi < M; ++mi) compute_item<NC>(ring[s][mi], u, b, nb, lds_qs, lds_bs, lds_d, acc[mi]);
+            if (cur.j == BPL - 1) {
+#pragma unroll
+                for (int mi = 0; mi < M; ++mi)
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) acc[mi].v[c] = group_sum<LPR>(acc[mi].v[c]);
+                if (cur.row < nrows) {
+#pragma unroll
+                    for (int c = 0; c < NC; ++c)
+                        if (lir == c) {
+                            if constexpr (M == 1) store(c, cur.row, acc[0].v[c]);
+                            else store(c, cur.row, acc[0].v[c], acc[1].v[c]);
+                        }
+                }
+#pragma unroll
+                for (int mi = 0; mi < M; ++mi)
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) acc[mi].v[c] = 0.f;
+            }
+            advance(cur);
+            if (cur.p >= npass) return;  // uniform over the wave
+        }
     }
+}
+
+// Streams rows [0, nrows) of one weight matrix (nb super-blocks per row, row_stride bytes apart) against
+// the NC columns staged in LDS; this wave takes passes wave, wave + nwaves, ... of 64/LPR rows each.
+// store(c, row, value) receives every row total of column c (called by one lane per row and column).
+// stage() runs on every wave of the workgroup after the wave's first weight loads are issued and
+// before the first item is computed: it fills the LDS columns (and ends with a workgroup barrier), so
+// the activation staging overlaps the weights' memory latency.
+template <int F, int NC, int LPR, int PF = GEMV_PF, class Stage, class Store>
+__device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int nrows, int nb, uint32_t row_stride, int wave,
+                                          int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs, const float *lds_d,
+                                          Stage stage, Store store) {
+    const uint8_t *const ws[1] = {w};
+    gemv_rows_m<F, NC, LPR, 1, PF>(ws, nrows, nb, row_stride, wave, nwaves, lds_qs, lds_bs, lds_d, stage, store);
+}
+
+// The same over two matrices of one shape at once: store(c, row, v0, v1) gets both row totals. Each
+// item already holds two blocks' loads, so a ring of two items keeps as many bytes in flight as the
+// single stream's three.
+template <int F, int NC, int LPR, int PF = 2, class Stage, class Store>
+__device__ __forceinline__ void gemv_rows2(const uint8_t *w0, const uint8_t *w1, int nrows, int nb, uint32_t row_stride,
+                                           int wave, int nwaves, const uint8_t *lds_qs, const int16_t *lds_bs,
+                                           const float *lds_d, Stage stage, Store store) {
+    const uint8_t *const ws[2] = {w0, w1};
+    gemv_rows_m<F, NC, LPR, 2, PF>(ws, nrows, nb, row_stride, wave, nwaves, lds_qs, lds_bs, lds_d, stage, store);
 }
 
 }  // namespace tq

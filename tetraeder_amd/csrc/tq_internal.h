@@ -99,6 +99,12 @@ struct MoeArgs {
     int64_t o_s1, o_s2;                // floats
 };
 hipError_t launch_moe_ffn(int type_gate, int type_up, int type_down, const MoeArgs &m, hipStream_t stream);
+// The whole step as one launch (one workgroup per CU, phases ordered by device-scope counters) when
+// moe_fused_supported says so; spin_limit bounds every wait (0: the default of about a second).
+bool moe_fused_supported(int type_gate, int type_up, const MoeArgs &m);
+hipError_t launch_moe_fused(int type_gate, int type_down, const MoeArgs &m, unsigned spin_limit, hipStream_t stream);
+// Failed waits recorded by the fused MoE launches on the current device since the last clear.
+hipError_t moe_sync_errors(unsigned *out, bool clear);
 hipError_t launch_swiglu(const float *gate, const float *up, float *out, int64_t n, hipStream_t stream);
 hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
                              int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream);

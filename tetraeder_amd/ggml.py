@@ -224,6 +224,13 @@ def moe_ffn(gate: QTensor, up: QTensor, down: QTensor, b: torch.Tensor, ids: tor
     return out
 
 
+def moe_sync_errors(clear: bool = False) -> int:
+    """Failed cross-workgroup waits of the single-launch MoE step on the current device (0: none)."""
+    v = C.c_uint(0)
+    _check(_lib.lib().tq_moe_ffn_sync_errors(C.byref(v), 1 if clear else 0))
+    return int(v.value)
+
+
 def moe_ffn_workspace_size(gate: QTensor, b: torch.Tensor, ids: torch.Tensor) -> int:
     gt, bt, it = gate.raw(), _dense(b, Type.F32), _dense(ids, Type.I32)
     return int(_lib.lib().tq_moe_ffn_workspace_size(C.byref(gt), C.byref(bt), C.byref(it)))
