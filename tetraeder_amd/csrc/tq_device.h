@@ -21,6 +21,13 @@ constexpr int Q8K_BSUMS = 260;
 
 enum Fmt { FMT_Q4K = 12, FMT_Q6K = 14 };
 
+// LDS layout of one staged Q8_K activation block (one column, one super-block) in the GEMV core: its
+// 256 qs bytes at a pitch of 272, so the column blocks one wave reads at once start 4 banks apart
+// (a 256-byte pitch put them all on the same banks: 8-way conflicts on every activation read); its
+// bsums in 72-byte slots (18 banks apart, conflict-free 8-byte reads); its d as one float.
+constexpr int ACT_QS_PITCH = 272;
+constexpr int ACT_BS_BYTES = 72;
+
 template <int F> struct FmtInfo;
 template <> struct FmtInfo<FMT_Q4K> { static constexpr int bytes = Q4K_BYTES; };
 template <> struct FmtInfo<FMT_Q6K> { static constexpr int bytes = Q6K_BYTES; };

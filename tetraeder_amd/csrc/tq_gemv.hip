@@ -17,8 +17,8 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3 + a.col0 * a.d_s1;
 
     uint8_t *lds_qs = lds;
-    int16_t *lds_bs = (int16_t *)(lds + NC * nb * 256);
-    float *lds_d = (float *)(lds + NC * nb * (256 + ACT_BS_BYTES));
+    int16_t *lds_bs = (int16_t *)(lds + NC * nb * ACT_QS_PITCH);
+    float *lds_d = (float *)(lds + NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES));
     auto stage = [&]() {
         if (a.b) {
             const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;

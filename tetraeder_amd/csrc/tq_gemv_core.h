@@ -24,7 +24,6 @@
 namespace tq {
 
 constexpr int GEMV_WAVES = 8;
-constexpr int ACT_BS_BYTES = 64;  // per (column, block): 8 lanes x up to 4 int16 bsums
 
 constexpr int LPB = 4;  // lanes per super-block
 
@@ -61,7 +60,7 @@ __device__ __forceinline__ void stage_activations(ColSrc col_src, int nb, int nc
         const int t = i & 63, cb = i >> 6, c = cb / nb, b = cb - c * nb;
         uint32_t v = 0;
         if (c < ncols) v = *(const uint32_t *)(col_src(c) + (size_t)b * Q8K_BYTES + Q8K_QS + 4 * t);
-        *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * t)) = v;
+        *(uint32_t *)(lds_qs + cb * ACT_QS_PITCH + act_perm<F>(4 * t)) = v;
     }
     constexpr int SLOTS = ActSlots<F>::n;
     const int nbs = NC * nb * LPB * SLOTS;
@@ -116,7 +115,7 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
         }
         d = __fdiv_rn(1.f, iscale);
     }
-    *(uint32_t *)(lds_qs + cb * 256 + act_perm<F>(4 * lane)) = packed;
+    *(uint32_t *)(lds_qs + cb * ACT_QS_PITCH + act_perm<F>(4 * lane)) = packed;
     sum += __shfl_xor(sum, 1, 64);
     sum += __shfl_xor(sum, 2, 64);  // lanes 4g..4g+3 hold the sum of 16-element group g
     if (F == FMT_Q4K) sum += __shfl_xor(sum, 4, 64);  // lanes 8g..8g+7: the 32-element sum of 2g, 2g+1
@@ -144,6 +143,17 @@ __device__ __forceinline__ void wave_quantize_to_lds(const float *__restrict__ s
     wave_quantize_vals_to_lds<F>(v, cb, lds_qs, lds_bs, lds_d);
 }
 
+// Zeroes the staged column blocks of columns ncols .. NC-1 (padding: zero scales, codes and sums give
+// zero contributions). All threads of the workgroup take part.
+template <int NC>
+__device__ __forceinline__ void zero_columns(int ncols, int nb, uint8_t *lds_qs, int16_t *lds_bs, float *lds_d) {
+    for (int i = ncols * nb + threadIdx.x; i < NC * nb; i += blockDim.x) lds_d[i] = 0.f;
+    for (int i = ncols * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x)
+        *(uint32_t *)(lds_qs + (i >> 6) * ACT_QS_PITCH + 4 * (i & 63)) = 0;
+    for (int i = ncols * nb * 16 + threadIdx.x; i < NC * nb * 16; i += blockDim.x)
+        lds_bs[(i >> 4) * (ACT_BS_BYTES / 2) + (i & 15)] = 0;
+}
+
 // Stages NC columns given as F32 rows (column c starts at col_f32(c), nb*256 floats; zeros for c >=
 // ncols), quantizing each 256-float block to Q8_K in LDS with one wave.
 template <int F, int NC, class ColF32>
@@ -154,10 +164,7 @@ __device__ __forceinline__ void stage_activations_f32(ColF32 col_f32, bool vec, 
         const int c = i / nb, b = i - c * nb;
         wave_quantize_to_lds<F>(col_f32(c) + (size_t)b * QK, vec, c * nb + b, lds_qs, lds_bs, lds_d);
     }
-    // padding columns: zero scales give zero contributions
-    for (int i = ncols * nb + threadIdx.x; i < NC * nb; i += blockDim.x) lds_d[i] = 0.f;
-    for (int i = ncols * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x) ((uint32_t *)lds_qs)[i] = 0;
-    for (int i = ncols * nb * 32 + threadIdx.x; i < NC * nb * 32; i += blockDim.x) lds_bs[i] = 0;
+    zero_columns<NC>(ncols, nb, lds_qs, lds_bs, lds_d);
 }
 
 template <int NC> struct Acc {
@@ -197,7 +204,12 @@ template <> struct Item<FMT_Q6K> {
         const uint32_t *ph = (const uint32_t *)(w + (o0 + 128 + 32 * h + 16 * v));
         const uint32_t *pt = (const uint32_t *)(w + (o0 + 192));
 #pragma unroll
-        for (int i = 0; i < 5; ++i) a[i] = pa[i], b[i] = pb[i], q[i] = ph[i], t[i] = pt[i];
+        for (int i = 0; i < 4; ++i) a[i] = pa[i], b[i] = pb[i], q[i] = ph[i];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) t[i] = pt[i];
+        // a window at a 4-byte boundary (every other block) needs no fifth dword: only the lanes whose
+        // block is 2 bytes off issue those loads
+        a[4] = pa[4], b[4] = pb[4], q[4] = ph[4];
     }
 };
 
@@ -227,7 +239,7 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
         const int cb = cb0 + col * nb;
-        const uint8_t *y = lds_qs + cb * 256 + u * 64;
+        const uint8_t *y = lds_qs + cb * ACT_QS_PITCH + u * 64;
         const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
         const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
         int slo = dot4(lo[0], y0.x, 0);
@@ -280,7 +292,7 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
         const int cb = cb0 + col * nb;
-        const uint8_t *y = lds_qs + cb * 256 + u * 64;
+        const uint8_t *y = lds_qs + cb * ACT_QS_PITCH + u * 64;
         const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
         const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
         const int S0 = dot4(c0[3], y0.w, dot4(c0[2], y0.z, dot4(c0[1], y0.y, dot4(c0[0], y0.x, 0))));

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include "tq_device.h"
 #include <stddef.h>
 #include <stdint.h>
 
@@ -55,7 +57,7 @@ struct MmqArgs {
     int64_t d_s1, d_s2, d_s3;  // float strides
 };
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
-constexpr size_t gemv_lds_per_col_block() { return 256 + 64 + 4; }
+constexpr size_t gemv_lds_per_col_block() { return ACT_QS_PITCH + ACT_BS_BYTES + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }
 
 // Lanes per weight row of a streaming GEMV over rows of nb super-blocks, and the waves a launch uses.

@@ -142,9 +142,9 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_gemv(MmidArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = a.nb;
     uint8_t *lds_qs = lds;
-    int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * 256);
-    float *lds_d = (float *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES));
-    int64_t *col_dst = (int64_t *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES + 4));
+    int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * ACT_QS_PITCH);
+    float *lds_d = (float *)(lds + MMID_NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES));
+    int64_t *col_dst = (int64_t *)(lds + MMID_NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES + 4));
     for (int c0 = 0; c0 < cnt; c0 += MMID_NC) {
         const int n = min(MMID_NC, cnt - c0);
         const int32_t *slots = slot + start + c0;
@@ -197,9 +197,9 @@ __device__ __forceinline__ void expert_columns(const uint8_t *w, int nrows, int 
                                                int cnt, Stage stage, DstOff dst_off, uint8_t *lds) {
     static_assert(NCM == 1 || NCM == 2 || NCM == 4 || NCM == 8, "columns per pass");
     uint8_t *lds_qs = lds;
-    int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * 256);
-    float *lds_d = (float *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES));
-    int64_t *col_dst = (int64_t *)(lds + MMID_NC * nb * (256 + ACT_BS_BYTES + 4));
+    int16_t *lds_bs = (int16_t *)(lds + MMID_NC * nb * ACT_QS_PITCH);
+    float *lds_d = (float *)(lds + MMID_NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES));
+    int64_t *col_dst = (int64_t *)(lds + MMID_NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES + 4));
     float *col_scale = (float *)(col_dst + MMID_NC);
     auto pass = [&](auto nct, int c0, int n) {
         constexpr int NC = decltype(nct)::value;
@@ -321,9 +321,7 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_moe_down(MoeArgs m) {
                                 silu_f32(gv.w) * uv.w};
             wave_quantize_vals_to_lds<F>(v, k * nb + blk, qs, bs, d);
         }
-        for (int i = n * nb + threadIdx.x; i < NC * nb; i += blockDim.x) d[i] = 0.f;
-        for (int i = n * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x) ((uint32_t *)qs)[i] = 0;
-        for (int i = n * nb * 32 + threadIdx.x; i < NC * nb * 32; i += blockDim.x) bs[i] = 0;
+        zero_columns<NC>(n, nb, qs, bs, d);
     };
     auto dst_off = [&](int k, int64_t &off, float &sc) {
         const int sl = g.cols[k], j = sl % m.n_used, t = sl / m.n_used;

@@ -181,8 +181,8 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
         const int P1 = (m.n_ff + RPW1 - 1) / RPW1;
         const int q0 = (int)((int64_t)P1 * k / nk), q1 = (int)((int64_t)P1 * (k + 1) / nk);
         uint8_t *lds_qs = lds;
-        int16_t *lds_bs = (int16_t *)(lds + MOE_NC * nb1 * 256);
-        float *lds_d = (float *)(lds + MOE_NC * nb1 * (256 + ACT_BS_BYTES));
+        int16_t *lds_bs = (int16_t *)(lds + MOE_NC * nb1 * ACT_QS_PITCH);
+        float *lds_d = (float *)(lds + MOE_NC * nb1 * (ACT_QS_PITCH + ACT_BS_BYTES));
         const int r0 = q0 * RPW1, nrows1 = max(0, min(m.n_ff - r0, (q1 - q0) * RPW1));
         const uint8_t *gw = m.gate + (int64_t)e * m.g_s2 + (int64_t)r0 * m.g_s1;
         const uint8_t *uw = m.up + (int64_t)e * m.u_s2 + (int64_t)r0 * m.u_s1;
@@ -213,8 +213,8 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
         constexpr int RPW2 = 64 / LPR2;
         const int P2 = (m.n_embd + RPW2 - 1) / RPW2;
         const int p0 = (int)((int64_t)P2 * k / nk), p1 = (int)((int64_t)P2 * (k + 1) / nk);
-        lds_bs = (int16_t *)(lds + MOE_NC * nb2 * 256);
-        lds_d = (float *)(lds + MOE_NC * nb2 * (256 + ACT_BS_BYTES));
+        lds_bs = (int16_t *)(lds + MOE_NC * nb2 * ACT_QS_PITCH);
+        lds_d = (float *)(lds + MOE_NC * nb2 * (ACT_QS_PITCH + ACT_BS_BYTES));
         const uint8_t *dw = m.down + (int64_t)e * m.dn_s2 + (int64_t)p0 * RPW2 * m.dn_s1;
         const int nrows2 = max(0, min(m.n_embd - p0 * RPW2, (p1 - p0) * RPW2));
         bool ready = false;
@@ -250,9 +250,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
                     for (int j = 0; j < 4; ++j) v[j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     wave_quantize_vals_to_lds<FD>(v, kk * nb2 + blk, lds_qs, lds_bs, lds_d);
                 }
-                for (int i = n * nb2 + threadIdx.x; i < NC * nb2; i += MOE_THREADS) lds_d[i] = 0.f;
-                for (int i = n * nb2 * 64 + threadIdx.x; i < NC * nb2 * 64; i += MOE_THREADS) ((uint32_t *)lds_qs)[i] = 0;
-                for (int i = n * nb2 * 32 + threadIdx.x; i < NC * nb2 * 32; i += MOE_THREADS) lds_bs[i] = 0;
+                zero_columns<NC>(n, nb2, lds_qs, lds_bs, lds_d);
                 if (threadIdx.x < NC) {
                     int64_t off = 0;
                     float sc = 0.f;
