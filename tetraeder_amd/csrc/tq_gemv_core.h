@@ -189,10 +189,11 @@ template <> struct Item<FMT_Q4K> {
 
 // Q6_K lane u = 2h + v covers elements 128h + 32k + 16v + 0..15, k = 0..3: 16-byte windows of ql at
 // 64h+16v and 64h+32+16v and of qh at 128+32h+16v, plus the scale/d tail at 192..209. A block starts
-// at an even address; every window is read as the aligned dwords that contain it (5 dwords per
-// window, 5 for the tail) and realigned by sh bytes.
+// at an even address; a window is realigned by sh bytes from the 4 aligned dwords at its start and the
+// fifth that follows, which is the first dword of another window of the same block (fetched from the
+// lane holding it in compute_item, so each lane issues 4 loads of 4 aligned dwords and 1 of 5).
 template <> struct Item<FMT_Q6K> {
-    uint32_t a[5], b[5], q[5], t[5], sh;
+    uint32_t a[4], b[4], q[4], t[5], sh;
     bool valid;
     // w is 4-byte aligned (checked by the host); off is the block's byte offset, even.
     __device__ __forceinline__ void load(const uint8_t *__restrict__ w, uint32_t off, int u) {
@@ -207,9 +208,6 @@ template <> struct Item<FMT_Q6K> {
         for (int i = 0; i < 4; ++i) a[i] = pa[i], b[i] = pb[i], q[i] = ph[i];
 #pragma unroll
         for (int i = 0; i < 5; ++i) t[i] = pt[i];
-        // a window at a 4-byte boundary (every other block) needs no fifth dword: only the lanes whose
-        // block is 2 bytes off issue those loads
-        a[4] = pa[4], b[4] = pb[4], q[4] = ph[4];
     }
 };
 
@@ -262,12 +260,25 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
                                              const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
     const int h = u >> 1, v = u & 1;
     const uint32_t sh = it.sh;
+    // Each window's fifth aligned dword is the first dword of another window of the same block, held by a
+    // lane of the same quad (lanes u = 0..3 of the block): a of (h, 0) runs into a of (h, 1), a of (h, 1)
+    // into b of (h, 0), b of (h, 0) into b of (h, 1), b of (0, 1) into a of (1, 0), b of (1, 1) into q of
+    // (0, 0), q of each lane into the next lane's q, q of (1, 1) into the tail. Quad permutes (DPP) fetch
+    // them: 5 moves and 4 selects instead of 3 load instructions.
+    const uint32_t xa = dpp_u<0xB1>(it.a[0]);  // quad_perm [1,0,3,2]
+    const uint32_t xb = dpp_u<0xB1>(it.b[0]);
+    const uint32_t pa = dpp_u<0xE8>(it.a[0]);  // quad_perm [0,2,2,3]: lane 1 <- lane 2
+    const uint32_t pq = dpp_u<0x24>(it.q[0]);  // quad_perm [0,1,2,0]: lane 3 <- lane 0
+    const uint32_t qq = dpp_u<0xF9>(it.q[0]);  // quad_perm [1,2,3,3]
+    const uint32_t a4 = v ? xb : xa;
+    const uint32_t b4 = u == 1 ? pa : u == 3 ? pq : xb;
+    const uint32_t q4 = u == 3 ? it.t[0] : qq;
     uint32_t A[4], B[4], H[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        A[i] = align_bytes(it.a[i + 1], it.a[i], sh);
-        B[i] = align_bytes(it.b[i + 1], it.b[i], sh);
-        H[i] = align_bytes(it.q[i + 1], it.q[i], sh);
+        A[i] = align_bytes(i == 3 ? a4 : it.a[i + 1], it.a[i], sh);
+        B[i] = align_bytes(i == 3 ? b4 : it.b[i + 1], it.b[i], sh);
+        H[i] = align_bytes(i == 3 ? q4 : it.q[i + 1], it.q[i], sh);
     }
     // scales[8h .. 8h+7] (this lane's four scales, bytes v, v+2, v+4, v+6 of them) and d
     const uint32_t s01 = h ? align_bytes(it.t[3], it.t[2], sh) : align_bytes(it.t[1], it.t[0], sh);
