@@ -154,11 +154,21 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // instead of the streaming GEMV (at most 8 columns per pass); below it the GEMV's shorter dependency
 // chain wins on decode shapes.
 constexpr int64_t MMQ_MIN_COLS = 64;
+// Q4_K from 4 to 64 columns: the skinny MFMA kernel (on MI355X q_proj 2048 -> 4096 at 4 / 16 / 32 / 64
+// columns: 8.1 / 8.5 / 10.0 / 13.1 us against 9.2 / 19.3 / 34.9 us for 8-column GEMV launches and 37.1 us
+// for the prefill kernel at 64).
+constexpr int64_t SKINNY_MIN_COLS = 4, SKINNY_MAX_COLS = 64;
 
-static bool use_mmq(int64_t ncols) { return ncols >= MMQ_MIN_COLS; }
+static bool use_skinny(int type, int64_t ncols) {
+    return ncols >= SKINNY_MIN_COLS && ncols <= SKINNY_MAX_COLS && skinny_supported(type, ncols);
+}
+static bool use_mmq(int type, int64_t ncols) { return ncols >= MMQ_MIN_COLS && !use_skinny(type, ncols); }
+
 
 // Decode-size F32 activations are quantized inside the GEMV workgroups (no workspace, one launch).
-static bool quantize_in_workgroup(int64_t ncols, int nb) { return !use_mmq(ncols) && ncols * nb <= 16; }
+static bool quantize_in_workgroup(int type, int64_t ncols, int nb) {
+    return !use_mmq(type, ncols) && !use_skinny(type, ncols) && ncols * nb <= 16;
+}
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
 
@@ -191,7 +201,7 @@ int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream) {
 }
 
 size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b) {
-    if (!a || !b || b->type != TQ_TYPE_F32 || quantize_in_workgroup(b->ne[1], (int)(a->ne[0] / QK))) return 0;
+    if (!a || !b || b->type != TQ_TYPE_F32 || quantize_in_workgroup(a->type, b->ne[1], (int)(a->ne[0] / QK))) return 0;
     return q8_bytes(b);
 }
 
@@ -220,16 +230,17 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
     if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
     const int nb = (int)(a->ne[0] / QK);
-    const bool mmq = use_mmq(b->ne[1]);
+    const bool mmq = use_mmq(a->type, b->ne[1]);
+    const bool skinny = use_skinny(a->type, b->ne[1]);
     const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
-    if (!mmq && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
+    if (!mmq && !skinny && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
     if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
 
     hipStream_t s = (hipStream_t)stream;
     void *q8 = b->data;
     // Small activations (decode) are quantized inside each GEMV workgroup, straight into LDS: one launch
     // instead of two. Larger ones get their own quantization pass first.
-    const bool in_wg = !pre_quantized && quantize_in_workgroup(b->ne[1], nb);
+    const bool in_wg = !pre_quantized && quantize_in_workgroup(a->type, b->ne[1], nb);
     if (!pre_quantized && !in_wg) {
         const size_t need = q8_bytes(b);
         if (workspace && workspace_size < need)
@@ -241,7 +252,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
                             "quantize_q8_K launch")))
             return rc;
     }
-    if (mmq) {
+    if (mmq || skinny) {
         MmqArgs m{};
         m.w = (const uint8_t *)a->data;
         m.nrows = a->ne[1];
@@ -259,6 +270,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         m.d_s1 = (int64_t)(dst->nb[1] / 4);
         m.d_s2 = (int64_t)(dst->nb[2] / 4);
         m.d_s3 = (int64_t)(dst->nb[3] / 4);
+        if (skinny) return check_hip(launch_skinny(a->type, m, s), "skinny launch");
         return check_hip(launch_mmq(a->type, m, s), "mmq launch");
     }
     GemvArgs g{};

@@ -57,6 +57,12 @@ struct MmqArgs {
     int64_t d_s1, d_s2, d_s3;  // float strides
 };
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
+
+// MUL_MAT for a few columns (batched decode) on int8 MFMA, weights read once for all columns: the same
+// operands as the prefill kernel, Q4_K weights, 1 <= ncols <= 64.
+using SkinnyArgs = MmqArgs;
+bool skinny_supported(int type, int64_t ncols);
+hipError_t launch_skinny(int type, const SkinnyArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return ACT_QS_PITCH + ACT_BS_BYTES + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }
 
