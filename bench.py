@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--moe-tokens", type=int, default=0, help="with --only moe: run just this token count")
-    p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill"], default=None,
+    p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill", "secondary"], default=None,
                    help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
                         "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
     return p.parse_args()
@@ -149,6 +149,9 @@ def main():
         return
     if args.only == "moe":
         print(json.dumps(bench_moe(ggml, torch, np, dev, tokens=(args.moe_tokens,) if args.moe_tokens else None)))
+        return
+    if args.only == "secondary":
+        print(json.dumps(bench_secondary(ggml, torch, dev)))
         return
     if args.only == "prefill":
         print(json.dumps(bench_prefill(ggml, torch, dev, only=os.environ.get("TQ_BENCH_PROFILE") == "1")))

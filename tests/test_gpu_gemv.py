@@ -171,3 +171,16 @@ def test_attention_projections(gpu, m):
         y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
         want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
         check(y, want, f"{name}_proj m={m}")
+
+
+@pytest.mark.parametrize("k,n,m", [(12288, 100, 20), (4096, 2048, 64), (256, 17, 4), (768, 2048, 33)])
+def test_q4_K_batched_decode_shapes(gpu, k, n, m):
+    """Q4_K with 4..64 columns runs the skinny MFMA kernel: long rows (48 super-blocks over 8 waves), a row
+    count that is no multiple of its 16-row tiles, and a column count that is no multiple of 16."""
+    _case(f"q4_K skinny k={k} n={n} m={m}")
+    ty = TYPES["q4_K"]
+    w = make_weights(ty, k, n, 1, seed=k + n + m, device=gpu)
+    x = normal((m, k), 7 * m + k)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q4_K k={k} n={n} m={m}")
