@@ -135,3 +135,41 @@ def test_prefill_shapes(gpu, name, tname, k, n, m):
     sub = w.data.view(n, rb)[torch.from_numpy(rows).to(gpu)].cpu().numpy().reshape(-1)
     want = O.mul_mat(ty.id, sub, k, len(rows), x)[0]
     check(y[:, rows], want, f"prefill {name} m={m}")
+
+
+@pytest.mark.parametrize("k,n,m", [(256, 256, 128), (768, 300, 130), (2048, 515, 257), (4096, 1000, 200),
+                                   (12288, 260, 129), (512, 256, 1000)])
+def test_mmq_tile_q4_K(gpu, k, n, m):
+    """Q4_K with at least 128 columns and 256 rows runs the 128 x 256 tile kernel: one tile, ragged last
+    tiles in both directions (computed over the last full window, stored only for their own rows), odd
+    and even super-block counts (the kernel walks super-blocks in pairs of LDS buffers), K up to 12288."""
+    _case(f"q4_K tile k={k} n={n} m={m}")
+    ty = TYPES["q4_K"]
+    w = make_weights(ty, k, n, 1, seed=k + 5 * n + 11 * m, device=gpu)
+    x = normal((m, k), k + 3 * n + 7 * m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q4_K tile k={k} n={n} m={m}")
+
+
+def test_mmq_tile_broadcast_strides_and_range(gpu):
+    """The tile kernel under broadcast (a [K, N, 2] over b [K, M, 4]), strided b and dst, columns over
+    1e-30 .. 1e30 and all-zero columns."""
+    _case("q4_K tile broadcast")
+    ty = TYPES["q4_K"]
+    k, n, m = 768, 300, 140
+    w = make_weights(ty, k, n, 2, seed=77, device=gpu)
+    xb = normal((4, m, k + 64), 78)
+    xb *= (10.0 ** np.linspace(-30, 30, m)).astype(np.float32)[None, :, None]
+    xb[1, 9] = 0.0
+    xt = torch.from_numpy(xb).to(gpu)[:, :, 32:32 + k]
+    out_big = torch.full((4, m, n + 8), float("nan"), device=gpu)
+    ggml.mul_mat(w, xt, out=out_big[:, :, :n])
+    got = out_big.cpu().numpy()
+    assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 32:32 + k]), ne2=2)
+    assert np.all(got[1, 9, :n] == 0)
+    for z in range(4):
+        for i in range(m):
+            if (z, i) != (1, 9):
+                check(got[z, i, :n], want[z, i], f"tile broadcast z={z} column {i}")
