@@ -60,6 +60,20 @@ __device__ __forceinline__ int moe_id(const MoeArgs &m, int s) {
     return e >= 0 && e < m.n_expert ? e : -1;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: DPP row shifts within each row of 16 lanes, then
+// the row totals (read lane by lane) added to the rows after them. No LDS round trips (a __shfl_up scan
+// is six of them).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31);
+    const int t2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row == 0 ? 0 : row == 1 ? t0 : row == 2 ? t0 + t1 : t0 + t1 + t2);
+}
+
 // Routing in LDS, identical in every workgroup: routed experts in increasing expert order, each with its
 // slots (in arbitrary order: every slot is an independent output column).
 __device__ void moe_route(const MoeArgs &m, MoeRoute &r) {
@@ -76,12 +90,7 @@ __device__ void moe_route(const MoeArgs &m, MoeRoute &r) {
         const int e0 = min(E, lane * chunk), e1 = min(E, e0 + chunk);
         int na = 0, ns = 0;
         for (int i = e0; i < e1; ++i) na += r.cnt[i] > 0, ns += r.cnt[i];
-        int pa = na, ps = ns;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int ya = __shfl_up(pa, off, 64), ys = __shfl_up(ps, off, 64);
-            if (lane >= off) pa += ya, ps += ys;
-        }
+        const int pa = wave_incl_scan(na), ps = wave_incl_scan(ns);
         int a = pa - na, p = ps - ns;
         for (int i = e0; i < e1; ++i) {
             const int c = r.cnt[i];
@@ -124,29 +133,104 @@ __device__ __forceinline__ int moe_cost(int cnt) {
 }
 
 // Deals the grid's workgroups to the routed experts: expert a gets workgroups [first[a], first[a+1]),
-// at least one each, the rest in proportion to moe_cost. Needs n_act <= gridDim.x. Returns this
-// workgroup's expert.
-__device__ int moe_deal(const MoeRoute &r, int *first, int *mine) {
+// at least one each. With four or more workgroups per expert on average, one each plus the rest in
+// proportion to moe_cost is within a few percent of the best whole-workgroup deal. With fewer, that
+// rounding leaves equal experts with 2 and 3 workgroups (at 16 tokens a 1.5x tail), so expert a gets
+// nk[a] = ceil(cost[a] / theta) for the smallest theta (work per workgroup) with sum nk <= G: the slowest
+// expert's workgroups then carry the least work any whole-workgroup deal allows. Wave 0 does it: the
+// classes of experts with equal token counts (the cost depends on the count only) come from ballots,
+// one per distinct count, and theta from two rounds of 64 geometric candidates, one per lane; nothing
+// waits on a shared-address atomic. Workgroups left over idle. Needs n_act <= G. cls has
+// 2 * MOE_MAX_SLOTS ints. Returns this workgroup's expert (-1: none).
+__device__ int moe_deal(const MoeRoute &r, int *first, int *cls, int *mine) {
+    constexpr int PER = (MOE_MAX_SLOTS + 63) / 64;  // routed experts per lane of wave 0
     const int n_act = r.n_act, nwg = gridDim.x;
     if (threadIdx.x < 64) {
-        const int lane = threadIdx.x, per = (n_act + 63) / 64, a0 = min(n_act, lane * per), a1 = min(n_act, a0 + per);
-        int c = 0;
-        for (int a = a0; a < a1; ++a) c += moe_cost(r.start[a + 1] - r.start[a]);
-        int pc = c;
+        const int lane = threadIdx.x;
+        if (4 * n_act > nwg) {
+            // this lane's experts lane * PER + i and their token counts (0: none)
+            int cnt[PER];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(pc, off, 64);
-            if (lane >= off) pc += y;
+            for (int i = 0; i < PER; ++i) {
+                const int a = lane * PER + i;
+                cnt[i] = a < n_act ? r.start[a + 1] - r.start[a] : 0;
+            }
+            // classes (count, experts) into cls, and the cost total and maximum, all uniform
+            int ncls = 0, ctot = 0, cmax = 0;
+            for (;;) {
+                int v = 0;
+#pragma unroll
+                for (int i = PER - 1; i >= 0; --i) v = cnt[i] ? cnt[i] : v;
+                const uint64_t any = __ballot(v != 0);
+                if (!any) break;
+                v = __builtin_amdgcn_readlane(v, __builtin_ctzll(any));
+                int n = 0;
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    n += __builtin_popcountll(__ballot(cnt[i] == v));
+                    if (cnt[i] == v) cnt[i] = 0;
+                }
+                const int c = moe_cost(v);
+                if (lane == 0) cls[2 * ncls] = c, cls[2 * ncls + 1] = n;
+                ++ncls, ctot += n * c, cmax = max(cmax, c);
+            }
+            // workgroups needed at work theta (every lane reads the classes it wrote from lane 0: one
+            // wave, program order)
+            auto need = [&](float theta) {
+                const float inv = 1.0f / theta;
+                int wgs = 0;
+                for (int k = 0; k < ncls; ++k) wgs += cls[2 * k + 1] * max(1, (int)ceilf((float)cls[2 * k] * inv));
+                return wgs;
+            };
+            // theta in (lo, hi]: hi = the largest cost is feasible (one workgroup each), below total / G
+            // is not
+            float lo = (float)ctot / (float)nwg * 0.999f, hi = (float)cmax;
+            for (int round = 0; round < 2 && hi > lo; ++round) {
+                const float step = __log2f(hi / lo) * (1.0f / 64.0f);
+                const float cand = lane == 63 ? hi : lo * exp2f(step * (float)(lane + 1));
+                const uint64_t ok = __ballot(need(cand) <= nwg);  // lane 63 (hi) is always feasible
+                const int j = __builtin_ctzll(ok);
+                const float new_hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cand), j));
+                const float new_lo =
+                    j ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cand), j - 1)) : lo;
+                hi = new_hi, lo = new_lo;
+            }
+            const float inv = 1.0f / hi;
+            int nk[PER], n = 0;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int a = lane * PER + i;
+                nk[i] = a < n_act ? max(1, (int)ceilf((float)moe_cost(r.start[a + 1] - r.start[a]) * inv)) : 0;
+                n += nk[i];
+            }
+            const int pn = wave_incl_scan(n);
+            // a sum past nwg (float rounding in the search) falls back to one workgroup each
+            const bool fits = __builtin_amdgcn_readlane(pn, 63) <= nwg;
+            int pre = fits ? pn - n : min(lane * PER, n_act);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int a = lane * PER + i;
+                if (a < n_act) first[a] = pre;
+                pre += fits ? nk[i] : (a < n_act);
+            }
+            if (lane == 63) first[n_act] = fits ? pn : n_act;
+        } else {
+            // one each, the spare in proportion to the cost prefix: first[a] = a + spare * pre(a) / total
+            const int per = (n_act + 63) / 64, a0 = min(n_act, lane * per), a1 = min(n_act, a0 + per);
+            int c = 0;
+            for (int a = a0; a < a1; ++a) c += moe_cost(r.start[a + 1] - r.start[a]);
+            const int pc = wave_incl_scan(c);
+            const int total = __builtin_amdgcn_readlane(pc, 63);
+            const int64_t spare = nwg - n_act;
+            int pre = pc - c;
+            for (int a = a0; a < a1; ++a) {
+                first[a] = a + (int)(spare * pre / total);
+                pre += moe_cost(r.start[a + 1] - r.start[a]);
+            }
+            if (lane == 63) first[n_act] = nwg;
         }
-        const int total = __shfl(pc, 63, 64);
-        const int64_t spare = nwg - n_act;
-        int pre = pc - c;
-        for (int a = a0; a < a1; ++a) {
-            first[a] = a + (int)(spare * pre / total);
-            pre += moe_cost(r.start[a + 1] - r.start[a]);
-        }
-        if (lane == 0) first[n_act] = nwg;
     }
+    if (threadIdx.x == 0) *mine = -1;
     __syncthreads();
     for (int a = threadIdx.x; a < n_act; a += MOE_THREADS)
         if (first[a] <= (int)blockIdx.x && (int)blockIdx.x < first[a + 1]) *mine = a;
@@ -158,6 +242,7 @@ template <int FG, int FU, int FD, int LPR1, int LPR2>
 __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned spin_limit) {
     __shared__ MoeRoute r;
     __shared__ int first[MOE_MAX_SLOTS + 1];
+    __shared__ int cls[2 * MOE_MAX_SLOTS];
     __shared__ int mine;
     __shared__ int64_t col_off[MOE_NC];
     __shared__ float col_scale[MOE_NC];
@@ -165,7 +250,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
     moe_route(m, r);
     const int n_act = r.n_act, n_slots = m.n_used * m.ntok;
     const int wave = threadIdx.x >> 6, wg = blockIdx.x;
-    const int a = n_act ? moe_deal(r, first, &mine) : -1;
+    const int a = n_act ? moe_deal(r, first, cls, &mine) : -1;  // -1 also for a workgroup left over
     float *act = m.gu;  // [n_slots][n_ff]
     unsigned exit_prev = 0;  // thread 0: the exit count before this workgroup's
     bool counted = false;    // this workgroup has counted itself out
