@@ -137,6 +137,21 @@ def test_prefill_shapes(gpu, name, tname, k, n, m):
     check(y[:, rows], want, f"prefill {name} m={m}")
 
 
+@pytest.mark.parametrize("k,n,m", [(256, 128, 128), (768, 300, 130), (2048, 515, 257), (4096, 1000, 200),
+                                   (12288, 130, 129), (512, 128, 1000), (1280, 129, 300)])
+def test_mmq_tile_q6_K(gpu, k, n, m):
+    """Q6_K with at least 128 columns and 128 rows runs the 128 x 128 tile kernel (planes built once per
+    workgroup in LDS): one tile, ragged last tiles in both directions, odd super-block counts (rows and
+    blocks that start 2 bytes past a dword boundary: Q6_K blocks are 210 bytes), K up to 12288."""
+    _case(f"q6_K tile k={k} n={n} m={m}")
+    ty = TYPES["q6_K"]
+    w = make_weights(ty, k, n, 1, seed=k + 5 * n + 13 * m, device=gpu)
+    x = normal((m, k), k + 3 * n + 5 * m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q6_K tile k={k} n={n} m={m}")
+
+
 @pytest.mark.parametrize("k,n,m", [(256, 256, 128), (768, 300, 130), (2048, 515, 257), (4096, 1000, 200),
                                    (12288, 260, 129), (512, 256, 1000)])
 def test_mmq_tile_q4_K(gpu, k, n, m):
@@ -152,11 +167,12 @@ def test_mmq_tile_q4_K(gpu, k, n, m):
     check(y, want, f"q4_K tile k={k} n={n} m={m}")
 
 
-def test_mmq_tile_broadcast_strides_and_range(gpu):
-    """The tile kernel under broadcast (a [K, N, 2] over b [K, M, 4]), strided b and dst, columns over
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+def test_mmq_tile_broadcast_strides_and_range(gpu, tname):
+    """The tile kernels under broadcast (a [K, N, 2] over b [K, M, 4]), strided b and dst, columns over
     1e-30 .. 1e30 and all-zero columns."""
-    _case("q4_K tile broadcast")
-    ty = TYPES["q4_K"]
+    _case(f"{tname} tile broadcast")
+    ty = TYPES[tname]
     k, n, m = 768, 300, 140
     w = make_weights(ty, k, n, 2, seed=77, device=gpu)
     xb = normal((4, m, k + 64), 78)

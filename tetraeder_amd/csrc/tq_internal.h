@@ -60,6 +60,9 @@ hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 // The large-tile prefill kernel (128 x 256 tiles, LDS-DMA staging); launch_mmq takes it when supported.
 bool mmq_tile_supported(int type, const MmqArgs &a);
 hipError_t launch_mmq_tile(int type, const MmqArgs &a, hipStream_t stream);
+// The Q6_K large-tile prefill kernel (128 x 128 tiles, planes built once per workgroup in LDS).
+bool mmq_tile_q6k_supported(const MmqArgs &a);
+hipError_t launch_mmq_tile_q6k(const MmqArgs &a, hipStream_t stream);
 
 // MUL_MAT for a few columns (batched decode) on int8 MFMA, weights read once for all columns: the same
 // operands as the prefill kernel, Q4_K weights, 1 <= ncols <= 64.

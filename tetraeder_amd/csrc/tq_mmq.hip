@@ -382,6 +382,7 @@ static hipError_t launch_fmt(const MmqArgs &a, hipStream_t stream) {
 
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream) {
     if (mmq_tile_supported(type, a)) return launch_mmq_tile(type, a, stream);
+    if (type == FMT_Q6K && mmq_tile_q6k_supported(a)) return launch_mmq_tile_q6k(a, stream);
     return type == FMT_Q4K ? launch_fmt<FMT_Q4K>(a, stream) : launch_fmt<FMT_Q6K>(a, stream);
 }
 
