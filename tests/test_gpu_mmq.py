@@ -189,3 +189,26 @@ def test_mmq_tile_broadcast_strides_and_range(gpu, tname):
         for i in range(m):
             if (z, i) != (1, 9):
                 check(got[z, i, :n], want[z, i], f"tile broadcast z={z} column {i}")
+
+
+@pytest.mark.parametrize("tname,k,n,m", [("q6_K", 4096, 256, 128), ("q4_K", 4096, 256, 130), ("q6_K", 3072, 300, 260)])
+def test_mmq_tile_k_split(gpu, tname, k, n, m):
+    """Few output tiles run split along k (several workgroups per tile, the last to arrive sums the
+    partials in split order): repeated calls give the same bits (the arrival counts reset, the order of
+    the sum does not depend on timing), the reported workspace holds the partials, a smaller one is
+    rejected, and the result matches the oracle."""
+    _case(f"{tname} k split k={k} n={n} m={m}")
+    ty = TYPES[tname]
+    w = make_weights(ty, k, n, 1, seed=k + n + m, device=gpu)
+    x = torch.from_numpy(normal((m, k), 3 * k + m)).to(gpu)
+    need = ggml.mul_mat_workspace_size(w, x)
+    assert need > m * (k // 256) * 292, "no room for the partial tiles"
+    runs = [ggml.mul_mat(w, x) for _ in range(3)]
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    runs.append(ggml.mul_mat(w, x, workspace=ws))
+    for r in runs[1:]:
+        assert torch.equal(r, runs[0])
+    with pytest.raises(ggml.Compute):
+        ggml.mul_mat(w, x, workspace=ws[: need - 256])
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x.cpu().numpy())[0]
+    check(runs[0].cpu().numpy(), want, f"{tname} k split")

@@ -172,6 +172,16 @@ static bool quantize_in_workgroup(int type, int64_t ncols, int nb) {
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
 
+// MUL_MAT's workspace: the Q8_K copy of an F32 b (none when b is Q8_K already or is quantized inside the
+// GEMV workgroups), then the partial tiles of a prefill launch split along k.
+static size_t mul_mat_q8_part(const tq_tensor *a, const tq_tensor *b) {
+    return b->type == TQ_TYPE_F32 && !quantize_in_workgroup(a->type, b->ne[1], (int)(a->ne[0] / QK)) ? q8_bytes(b) : 0;
+}
+static size_t mul_mat_split_part(const tq_tensor *a, const tq_tensor *b) {
+    if (!use_mmq(a->type, b->ne[1])) return 0;
+    return align_up(mmq_split_bytes(a->type, b->ne[1], a->ne[1], (int)(a->ne[0] / QK), (int)(b->ne[2] * b->ne[3])), 256);
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -201,8 +211,8 @@ int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream) {
 }
 
 size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b) {
-    if (!a || !b || b->type != TQ_TYPE_F32 || quantize_in_workgroup(a->type, b->ne[1], (int)(a->ne[0] / QK))) return 0;
-    return q8_bytes(b);
+    if (!a || !b || (b->type != TQ_TYPE_F32 && b->type != TQ_TYPE_Q8_K) || a->ne[0] % QK) return 0;
+    return mul_mat_q8_part(a, b) + mul_mat_split_part(a, b);
 }
 
 int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
@@ -241,12 +251,17 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     // Small activations (decode) are quantized inside each GEMV workgroup, straight into LDS: one launch
     // instead of two. Larger ones get their own quantization pass first.
     const bool in_wg = !pre_quantized && quantize_in_workgroup(a->type, b->ne[1], nb);
-    if (!pre_quantized && !in_wg) {
-        const size_t need = q8_bytes(b);
+    const size_t q8_need = mul_mat_q8_part(a, b), split_need = mul_mat_split_part(a, b);
+    uint8_t *ws = nullptr;
+    if (q8_need + split_need) {
+        const size_t need = q8_need + split_need;
         if (workspace && workspace_size < need)
             return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-        q8 = workspace ? workspace : own_workspace(need, &rc);
-        if (!q8) return rc;
+        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+        if (!ws) return rc;
+    }
+    if (!pre_quantized && !in_wg) {
+        q8 = ws;
         if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], b->ne[3], b->nb[1],
                                                  b->nb[2], b->nb[3], q8, s),
                             "quantize_q8_K launch")))
@@ -270,6 +285,10 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         m.d_s1 = (int64_t)(dst->nb[1] / 4);
         m.d_s2 = (int64_t)(dst->nb[2] / 4);
         m.d_s3 = (int64_t)(dst->nb[3] / 4);
+        if (split_need) {
+            m.ksplit = mmq_tile_split(a->type, m.ncols, m.nrows, nb, m.nbatch);
+            m.part = (float *)(ws + q8_need);
+        }
         if (skinny) return check_hip(launch_skinny(a->type, m, s), "skinny launch");
         return check_hip(launch_mmq(a->type, m, s), "mmq launch");
     }

@@ -55,10 +55,16 @@ struct MmqArgs {
     int32_t ncols;       // M
     float *dst;          // dst[m*d_s1 + n] of batch (i2,i3) at dst + i2*d_s2 + i3*d_s3
     int64_t d_s1, d_s2, d_s3;  // float strides
+    int32_t ksplit;      // tile kernels: workgroups per output tile along k (1: none)
+    float *part;         // ksplit > 1: workspace of mmq_split_bytes for the partial tiles
 };
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 // The large-tile prefill kernel (128 x 256 tiles, LDS-DMA staging); launch_mmq takes it when supported.
 bool mmq_tile_supported(int type, const MmqArgs &a);
+// k split of the tile kernels for an output of ncols x nrows x nbatch over nb super-blocks (1: none) and
+// the workspace bytes its partial tiles take
+int mmq_tile_split(int type, int64_t ncols, int64_t nrows, int nb, int nbatch);
+size_t mmq_split_bytes(int type, int64_t ncols, int64_t nrows, int nb, int nbatch);
 hipError_t launch_mmq_tile(int type, const MmqArgs &a, hipStream_t stream);
 // The Q6_K large-tile prefill kernel (128 x 128 tiles, planes built once per workgroup in LDS).
 bool mmq_tile_q6k_supported(const MmqArgs &a);

@@ -24,6 +24,7 @@
 // weight row l % 32 (one scale set per lane) and activation rows 8 (v / 4) + 4 (l / 32) + v % 4.
 #include "tq_device.h"
 #include "tq_internal.h"
+#include "tq_mmq_split.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -66,6 +67,9 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *
 // consecutive rows 8 distinct slots (32 banks).
 __device__ __forceinline__ int bkey(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// arrival counts of the k split's output tiles
+__device__ unsigned g_tile_q4k_arrivals[MMQ_MAX_SPLIT_TILES];
+
 }  // namespace
 
 __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
@@ -85,8 +89,9 @@ __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
     // go to one XCD when the tile count allows
     const int tiles_m = (a.ncols + TL_TM - 1) / TL_TM, tiles_n = (int)((a.nrows + TL_TN - 1) / TL_TN);
     const int ntiles = tiles_m * tiles_n;
-    int t = blockIdx.x;
-    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    const int S = a.ksplit > 1 ? a.ksplit : 1;  // workgroups per tile along k
+    int t, split;
+    mmq_tile_and_split(ntiles, S, t, split);
     constexpr int GM = 4;
     const int gsize = GM * tiles_n, grp = t / gsize, first_m = grp * GM;
     const int gm = min(tiles_m - first_m, GM), tr = t - grp * gsize;
@@ -97,9 +102,11 @@ __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
     const int64_t n_own = (int64_t)nt * TL_TN, n0 = min(n_own, a.nrows - TL_TN);
 
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
-    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3 + n0 * a.row_stride;
-    const int nb = a.nb;
-    const uint8_t *q8 = a.q8 + ((int64_t)blockIdx.y * a.ncols + m0) * nb * Q8K_BYTES;
+    // this workgroup's super-blocks [kb0, kb0 + nbk) of the nb per row
+    const int nb = a.nb, kb0 = split * nb / S, nbk = (split + 1) * nb / S - kb0;
+    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3 + n0 * a.row_stride +
+                       (int64_t)kb0 * Q4K_BYTES;
+    const uint8_t *q8 = a.q8 + ((int64_t)blockIdx.y * a.ncols + m0) * nb * Q8K_BYTES + (int64_t)kb0 * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
     const uint32_t a_row = (uint32_t)nb * Q8K_BYTES, b_row = (uint32_t)a.row_stride;
 
@@ -172,7 +179,7 @@ __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
 
     auto superblock = [&](auto cur_c, int b) {
         constexpr int CUR = decltype(cur_c)::value;
-        const bool more = b + 1 < nb;
+        const bool more = b + 1 < nbk;
         if (more) stage_issue(std::integral_constant<int, CUR ^ 1>{}, b + 1);
 
         const uint8_t *aq = (CUR ? s_aq1 : s_aq0) + (wm * 64 + l32) * 256;
@@ -283,9 +290,30 @@ __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
     stage_issue(std::integral_constant<int, 0>{}, 0);
     stage_finish(0);
     __syncthreads();
-    for (int b = 0; b < nb; b += 2) {
+    for (int b = 0; b < nbk; b += 2) {
         superblock(std::integral_constant<int, 0>{}, b);
-        if (b + 1 < nb) superblock(std::integral_constant<int, 1>{}, b + 1);
+        if (b + 1 < nbk) superblock(std::integral_constant<int, 1>{}, b + 1);
+    }
+
+    if (S > 1) {
+        __shared__ int arrival;
+        float v[TL_FM * TL_FN * 16];
+#pragma unroll
+        for (int fm = 0; fm < TL_FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < TL_FN; ++fn)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[(fm * TL_FN + fn) * 16 + i] = acc[fm][fn][i];
+        const int gt = blockIdx.y * ntiles + t;
+        if (!mmq_split_reduce<TL_FM * TL_FN * 16, TL_THREADS>(v, a.part + (int64_t)gt * S * TL_TM * TL_TN, split, S,
+                                                              &g_tile_q4k_arrivals[gt], &arrival))
+            return;
+#pragma unroll
+        for (int fm = 0; fm < TL_FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < TL_FN; ++fn)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[fm][fn][i] = v[(fm * TL_FN + fn) * 16 + i];
     }
 
     const int64_t d_s1 = a.d_s1;
@@ -315,9 +343,54 @@ bool mmq_tile_supported(int type, const MmqArgs &a) {
 hipError_t launch_mmq_tile(int type, const MmqArgs &a, hipStream_t stream) {
     if (!mmq_tile_supported(type, a)) return hipErrorNotSupported;
     const int64_t tiles = (int64_t)((a.ncols + TL_TM - 1) / TL_TM) * ((a.nrows + TL_TN - 1) / TL_TN);
-    if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-    k_mmq_tile_q4k<<<dim3((unsigned)tiles, (unsigned)a.nbatch), TL_THREADS, 0, stream>>>(a);
+    const int S = a.ksplit > 1 ? a.ksplit : 1;
+    if (tiles * S > 0x7fffffff) return hipErrorInvalidValue;
+    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
+        return hipErrorInvalidValue;
+    k_mmq_tile_q4k<<<dim3((unsigned)(tiles * S), (unsigned)a.nbatch), TL_THREADS, 0, stream>>>(a);
     return hipGetLastError();
+}
+
+// Output tile of the tile kernels by weight type, and the time one workgroup takes per super-block
+// (MI355X: 5.5 us for a Q4_K 128 x 256 tile, 3.4 us for a Q6_K 128 x 128 tile)
+static void tile_shape(int type, int &tm, int &tn, double &us_per_sb) {
+    if (type == FMT_Q4K) tm = TL_TM, tn = TL_TN, us_per_sb = 5.5;
+    else tm = 128, tn = 128, us_per_sb = 3.4;  // k_mmq_tile_q6k
+}
+
+int mmq_tile_split(int type, int64_t ncols, int64_t nrows, int nb, int nbatch) {
+    int tm, tn;
+    double us_sb;
+    tile_shape(type, tm, tn, us_sb);
+    if (ncols < tm || nrows < tn) return 1;
+    const int64_t tiles = ((ncols + tm - 1) / tm) * ((nrows + tn - 1) / tn) * nbatch;
+    if (tiles > MMQ_MAX_SPLIT_TILES) return 1;
+    // One workgroup per CU at a time (LDS). Time = rounds of workgroups x (super-blocks per workgroup x
+    // us_sb + about 2 us of start-up) + the partial tiles' traffic (each written once and, but for the
+    // last arrival's own, read once) at about 6 TB/s. On MI355X this picks 2 for the Q6_K 12288 -> 4096
+    // projection at 512 columns (128 tiles: 159 -> 94 us) and none for Q4_K 4096 -> 12288 at 512 (192 tiles:
+    // 4 splits measured 122 us against 89).
+    const int64_t cus = device_cu_count();
+    const double tile_bytes = (double)tm * tn * sizeof(float);
+    int best = 1;
+    double best_us = 0;
+    for (int S = 1; S <= MMQ_MAX_SPLIT && nb / S >= 2; ++S) {
+        const double rounds = (double)((tiles * S + cus - 1) / cus);
+        double us = rounds * ((nb + S - 1) / S * us_sb + 2.0);
+        if (S > 1) us += (double)tiles * tile_bytes * (2.0 * S - 1.0) / 6.0e6;
+        if (S == 1 || us < best_us) best = S, best_us = us;
+    }
+    return best;
+}
+
+size_t mmq_split_bytes(int type, int64_t ncols, int64_t nrows, int nb, int nbatch) {
+    const int S = mmq_tile_split(type, ncols, nrows, nb, nbatch);
+    if (S <= 1) return 0;
+    int tm, tn;
+    double us_sb;
+    tile_shape(type, tm, tn, us_sb);
+    const size_t tiles = (size_t)((ncols + tm - 1) / tm) * ((nrows + tn - 1) / tn) * nbatch;
+    return tiles * S * tm * tn * sizeof(float);
 }
 
 }  // namespace tq

@@ -22,6 +22,7 @@
 // 32-deep step; output lane l holds weight row l % 32 and activation rows 8 (v / 4) + 4 (l / 32) + v % 4.
 #include "tq_device.h"
 #include "tq_internal.h"
+#include "tq_mmq_split.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -42,10 +43,14 @@ constexpr int T6_PPITCH = 144;              // LDS bytes per weight row of a pla
 constexpr int T6_RAW = 128;                 // LDS bytes per weight row of a half's raw pieces
 static_assert(T6_TM * 8 == 2 * 64 * T6_WAVES && T6_TN * 8 == 2 * 64 * T6_WAVES, "two 1 KB wave loads each");
 static_assert(T6_TN * 8 == 2 * T6_THREADS, "two expansion tasks per thread");
+static_assert(T6_TM == 128 && T6_TN == 128, "the k split's tile shape (mmq_tile_split)");
 
 // slot key of a row's pieces: 16 consecutive rows at one piece get 16 distinct (r & 1, slot) pairs
 // (distinct banks of a 64-bank LDS at a 128-byte pitch) and 8 aligned consecutive rows 8 distinct slots
 __device__ __forceinline__ int rkey(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// arrival counts of the k split's output tiles
+__device__ unsigned g_tile_q6k_arrivals[MMQ_MAX_SPLIT_TILES];
 
 }  // namespace
 
@@ -68,8 +73,9 @@ __global__ __launch_bounds__(T6_THREADS, 1) void k_mmq_tile_q6k(MmqArgs a) {
     // and stores only its own rows
     const int tiles_m = (a.ncols + T6_TM - 1) / T6_TM, tiles_n = (int)((a.nrows + T6_TN - 1) / T6_TN);
     const int ntiles = tiles_m * tiles_n;
-    int t = blockIdx.x;
-    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    const int S = a.ksplit > 1 ? a.ksplit : 1;  // workgroups per tile along k
+    int t, split;
+    mmq_tile_and_split(ntiles, S, t, split);
     constexpr int GM = 4;
     const int gsize = GM * tiles_n, grp = t / gsize, first_m = grp * GM;
     const int gm = min(tiles_m - first_m, GM), tr = t - grp * gsize;
@@ -78,9 +84,11 @@ __global__ __launch_bounds__(T6_THREADS, 1) void k_mmq_tile_q6k(MmqArgs a) {
     const int64_t n_own = (int64_t)nt * T6_TN, n0 = min(n_own, a.nrows - T6_TN);
 
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
-    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3 + n0 * a.row_stride;
-    const int nb = a.nb, nh = 2 * nb;
-    const uint8_t *q8 = a.q8 + ((int64_t)blockIdx.y * a.ncols + m0) * nb * Q8K_BYTES;
+    // this workgroup's super-blocks [kb0, kb0 + nbk) of the nb per row, nh halves
+    const int nb = a.nb, kb0 = split * nb / S, nbk = (split + 1) * nb / S - kb0, nh = 2 * nbk;
+    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3 + n0 * a.row_stride +
+                       (int64_t)kb0 * Q6K_BYTES;
+    const uint8_t *q8 = a.q8 + ((int64_t)blockIdx.y * a.ncols + m0) * nb * Q8K_BYTES + (int64_t)kb0 * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
     const int64_t a_row = (int64_t)nb * Q8K_BYTES;
 
@@ -236,16 +244,33 @@ __global__ __launch_bounds__(T6_THREADS, 1) void k_mmq_tile_q6k(MmqArgs a) {
         using Q = std::integral_constant<int, P ^ 1>;
         if (h + 1 < nh) dma_a(Q{}, h + 1);
         if (h + 2 < nh) dma_raw(hpar_c, h + 2);
-        if (P == 0 && (h >> 1) + 1 < nb) load_scalars((h >> 1) + 1);
+        if (P == 0 && (h >> 1) + 1 < nbk) load_scalars((h >> 1) + 1);
         if (h + 1 < nh) expand(Q{}, Q{}, h + 1);
         mfma_half(hpar_c, hpar_c, P == 0);
         if (P == 1) combine(h >> 1);
-        if (P == 0 && (h >> 1) + 1 < nb) store_scalars(((h >> 1) + 1) & 1);
+        if (P == 0 && (h >> 1) + 1 < nbk) store_scalars(((h >> 1) + 1) & 1);
         __syncthreads();
     };
     for (int h = 0; h < nh; h += 2) {
         step(I0{}, h);
         step(I1{}, h + 1);
+    }
+
+    if (S > 1) {
+        __shared__ int arrival;
+        float v[T6_FM * 16];
+#pragma unroll
+        for (int fm = 0; fm < T6_FM; ++fm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[fm * 16 + i] = acc[fm][i];
+        const int gt = blockIdx.y * ntiles + t;
+        if (!mmq_split_reduce<T6_FM * 16, T6_THREADS>(v, a.part + (int64_t)gt * S * T6_TM * T6_TN, split, S,
+                                                      &g_tile_q6k_arrivals[gt], &arrival))
+            return;
+#pragma unroll
+        for (int fm = 0; fm < T6_FM; ++fm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[fm][i] = v[fm * 16 + i];
     }
 
     const int64_t d_s1 = a.d_s1;
@@ -271,8 +296,11 @@ bool mmq_tile_q6k_supported(const MmqArgs &a) {
 hipError_t launch_mmq_tile_q6k(const MmqArgs &a, hipStream_t stream) {
     if (!mmq_tile_q6k_supported(a)) return hipErrorNotSupported;
     const int64_t tiles = (int64_t)((a.ncols + T6_TM - 1) / T6_TM) * ((a.nrows + T6_TN - 1) / T6_TN);
-    if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-    k_mmq_tile_q6k<<<dim3((unsigned)tiles, (unsigned)a.nbatch), T6_THREADS, 0, stream>>>(a);
+    const int S = a.ksplit > 1 ? a.ksplit : 1;
+    if (tiles * S > 0x7fffffff) return hipErrorInvalidValue;
+    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
+        return hipErrorInvalidValue;
+    k_mmq_tile_q6k<<<dim3((unsigned)(tiles * S), (unsigned)a.nbatch), T6_THREADS, 0, stream>>>(a);
     return hipGetLastError();
 }
 
