@@ -28,6 +28,10 @@ enum Fmt { FMT_Q4K = 12, FMT_Q6K = 14 };
 constexpr int ACT_QS_PITCH = 272;
 constexpr int ACT_BS_BYTES = 72;
 
+// Word 3 of a raw buffer resource on gfx9: 32-bit data format, no swizzle, no per-lane index added.
+// A raw buffer load with an offset at or beyond the resource's byte count loads nothing (zeros).
+constexpr int BUFFER_FLAGS = 0x00020000;
+
 template <int F> struct FmtInfo;
 template <> struct FmtInfo<FMT_Q4K> { static constexpr int bytes = Q4K_BYTES; };
 template <> struct FmtInfo<FMT_Q6K> { static constexpr int bytes = Q6K_BYTES; };

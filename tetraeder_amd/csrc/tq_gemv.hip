@@ -40,6 +40,61 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
                           });
 }
 
+// The most super-blocks a row streamed through the LDS slots can have, and the activation bytes that many
+// take: the activations are a static array too, so that the compiler can tell their reads from the
+// slots' in-flight loads (it makes a read of memory it cannot tell apart wait for every DMA).
+template <int F, int LPR> constexpr int gemv_dma_max_nb() {
+    return GEMV_DMA_SLOT / ((64 / LPR) * (F == FMT_Q4K ? Q4K_BYTES : Q6K_BYTES));
+}
+constexpr int GEMV_DMA_MAX_NC = 4;
+
+// The same over contiguous rows through wave-private LDS slots (gemv_rows_dma).
+template <int F, int NC, int LPR>
+__global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv_dma(GemvArgs a) {
+    static_assert(NC <= GEMV_DMA_MAX_NC, "columns of the LDS stream");
+    __shared__ __align__(16) uint8_t slot0[GEMV_WAVES][GEMV_DMA_SLOT], slot1[GEMV_WAVES][GEMV_DMA_SLOT],
+        slot2[GEMV_WAVES][GEMV_DMA_SLOT];
+    __shared__ float stash[GEMV_WAVES][GEMV_DMA_STASH];
+    __shared__ __align__(16) uint8_t lds[NC * gemv_dma_max_nb<F, LPR>() * gemv_lds_per_col_block()];
+    const int nb = a.nb, wv = threadIdx.x >> 6;
+    const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
+    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
+    const uint8_t *q8 = a.q8 + ((int64_t)(i3 * a.ne12 + i2) * a.q8_cols + a.col0) * nb * Q8K_BYTES;
+    float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3 + a.col0 * a.d_s1;
+
+    uint8_t *lds_qs = lds;
+    int16_t *lds_bs = (int16_t *)(lds + NC * nb * ACT_QS_PITCH);
+    float *lds_d = (float *)(lds + NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES));
+    auto stage = [&]() {
+        if (a.b) {
+            const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;
+            const int64_t b_s1 = a.b_s1;
+            stage_activations_f32<F, NC>([&](int c) { return b + c * b_s1; }, a.b_vec != 0, nb, a.ncols, lds_qs,
+                                         lds_bs, lds_d);
+        } else {
+            const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
+            stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
+        }
+        __syncthreads();
+    };
+
+    const int ncols = a.ncols;
+    const int64_t d_s1 = a.d_s1;
+    gemv_rows_dma<F, NC, LPR>(w, (int)a.nrows, nb, blockIdx.x * GEMV_WAVES + wv, gridDim.x * GEMV_WAVES, slot0[wv],
+                              slot1[wv], slot2[wv], stash[wv], lds_qs, lds_bs, lds_d, stage, [&](int c, int row, float v) {
+                                  if (c < ncols) dst[c * d_s1 + row] = v;
+                              });
+}
+
+// The LDS stream takes contiguous rows whose row bytes are a multiple of 16 (every wave load of 16-byte
+// pieces stays inside the pass), a pass within one slot, a matrix below 4 GiB and dword-aligned bases.
+static bool gemv_dma_ok(int type, const GemvArgs &a, int lpr) {
+    const int64_t rb = (int64_t)a.nb * (type == FMT_Q4K ? Q4K_BYTES : Q6K_BYTES);
+    return a.row_stride == rb && rb % 16 == 0 && (64 / lpr) * rb <= GEMV_DMA_SLOT && a.nrows * rb < (1ll << 32) &&
+           (lpr == 16 || lpr == 32 || lpr == 64) &&
+           ((uintptr_t)a.w & 15) == 0 && a.w_s2 % 16 == 0 && a.w_s3 % 16 == 0;
+}
+
 // Lanes per row (a power of two from 4 to 64, at least nc: lanes 0 .. nc-1 of a row store its column
 // totals): a row's super-blocks are spread over LPR / 4 lane groups, and the most lanes per row that
 // leave no group idle are taken, so one wave load instruction covers 64 / LPR whole rows: a contiguous
@@ -71,6 +126,16 @@ static hipError_t launch_nc(const GemvArgs &a, hipStream_t stream) {
     const int64_t npass = (a.nrows + rpw - 1) / rpw;
     const int64_t waves = std::min<int64_t>(npass, gemv_stream_waves());
     const dim3 g2((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES), (unsigned)a.nbatch);
+    if constexpr (NC <= GEMV_DMA_MAX_NC) {
+        if (gemv_dma_ok(F, a, lpr)) {
+            switch (lpr) {
+            case 16: k_gemv_dma<F, NC, 16><<<g2, GEMV_WAVES * 64, 0, stream>>>(a); break;
+            case 32: k_gemv_dma<F, NC, 32><<<g2, GEMV_WAVES * 64, 0, stream>>>(a); break;
+            default: k_gemv_dma<F, NC, 64><<<g2, GEMV_WAVES * 64, 0, stream>>>(a); break;
+            }
+            return hipGetLastError();
+        }
+    }
     switch (lpr) {
     case 4:
         if constexpr (NC <= 4) k_gemv<F, NC, 4><<<g2, GEMV_WAVES * 64, lds, stream>>>(a);

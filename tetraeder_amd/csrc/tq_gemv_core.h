@@ -428,6 +428,116 @@ __device__ __forceinline__ void gemv_rows_m(const uint8_t *const (&ws)[M], int n
     }
 }
 
+// The same stream for a matrix of contiguous rows whose row bytes are a multiple of 16, through LDS: a
+// wave pass (64 / LPR whole rows, at most GEMV_DMA_SLOT bytes) goes global -> LDS in 1 KB wave loads
+// (buffer_load_dwordx4 ... lds, non-temporal) into one of three slots private to the wave, two passes
+// ahead of the one being computed, and every lane then reads its items from the slot. Each cache line
+// of the matrix is fetched by one wave load and no register holds data in flight. A wave reads only
+// what it loaded itself: no barrier, only its own load counter. The slots are three distinct LDS arrays
+// (the loop is unrolled three times), so the compiler waits for the one fill a read needs and not for
+// the two behind it; for that it must know how many loads were issued after it, so every fill issues
+// the same four wave loads, branch-free, and lanes past the pass (or fills past the last pass) take an
+// offset beyond the buffer's range, which loads nothing. (Buffer loads, not global ones: the compiler
+// makes every LDS read after a global_load_lds wait for all loads in flight.)
+constexpr int GEMV_DMA_SLOT = 4096;
+constexpr int WAIT_VMCNT_8 = 0x0F78;  // s_waitcnt vmcnt(8): expcnt and lgkmcnt at their maxima (no wait)
+constexpr int GEMV_DMA_STASH = 256;  // floats of row totals per wave
+
+template <int F, int NC, int LPR, class Stage, class Store>
+__device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int nb, int wave, int nwaves, uint8_t *slot0,
+                                              uint8_t *slot1, uint8_t *slot2, float *stash, const uint8_t *lds_qs,
+                                              const int16_t *lds_bs, const float *lds_d, Stage stage, Store store) {
+    constexpr int G = LPR / LPB;   // super-blocks of a row per wave pass
+    constexpr int RPW = 64 / LPR;  // rows per wave pass
+    constexpr int BYTES = FmtInfo<F>::bytes;
+    static_assert(GEMV_DMA_SLOT / (RPW * BYTES) <= 2 * G, "a row that fits a slot has at most two items per lane");
+    const int lane = lane_id();
+    const int u = lane % LPB, gb = (lane % LPR) / LPB, lrow = lane / LPR, lir = lane % LPR;
+    const int npass = (nrows + RPW - 1) / RPW, BPL = (nb + G - 1) / G;
+    const uint32_t rb = (uint32_t)nb * BYTES, span = RPW * rb, total = (uint32_t)nrows * rb;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)w, (short)0, (int)total, BUFFER_FLAGS);
+    auto dma = [&](uint8_t *slot, int p) {
+        const bool real = p < npass;
+        const uint32_t start = real ? (uint32_t)p * span : 0u, len = real ? min(span, total - start) : 0u;
+#pragma unroll
+        for (int c = 0; c < GEMV_DMA_SLOT / 1024; ++c) {
+            const uint32_t off = 1024 * c + 16 * lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(slot + 1024 * c), 16,
+                                                     off < len ? start + off : total, 0, 0, 2 /* non-temporal */);
+        }
+    };
+    const bool active = wave < npass;  // uniform over the wave
+    if (active) {
+        dma(slot0, wave);
+        dma(slot1, wave + nwaves);
+    }
+    stage();
+    if (!active) return;
+    // Row totals wait in the wave's stash until it is full or the stream ends: a store among the loads
+    // would make the compiler wait for every load in flight (it cannot order the two kinds of access).
+    constexpr int STASH_PASSES = GEMV_DMA_STASH / (RPW * NC);
+    static_assert(STASH_PASSES >= 3, "stash of at least one unrolled step");
+    int k = 0;
+    auto pass = [&](const uint8_t *slot, int p) {
+        // this pass's fill is complete once at most the two fills issued after it are in flight (the
+        // compiler's own count of LDS fills is not trusted across the loop's back edge)
+        __builtin_amdgcn_s_waitcnt(WAIT_VMCNT_8);
+        asm volatile("" ::: "memory");
+        Acc<NC> acc;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
+        const int row = p * RPW + lrow;
+        // a pass fits one slot, so a row has at most 2 * G super-blocks: straight-line items keep each LDS
+        // read's address a fixed offset from its slot, which lets the compiler wait for that slot's DMA only
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (j >= BPL) break;
+            const int b = gb + j * G;
+            Item<F> it;
+            it.valid = row < nrows && b < nb;
+            // an invalid item reads the pass's first block, which the pass always holds
+            it.load(slot, it.valid ? (uint32_t)lrow * rb + (uint32_t)(b * BYTES) : 0u, u);
+            compute_item<NC>(it, u, min(b, nb - 1), nb, lds_qs, lds_bs, lds_d, acc);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (lir == c) stash[k * (RPW * NC) + lrow * NC + c] = acc.v[c];
+        ++k;
+    };
+    // the k stashed passes, the first being pass p0, go to store()
+    auto flush = [&](int p0) {
+        for (int i = lane; i < k * (RPW * NC); i += 64) {
+            const int kk = i / (RPW * NC), r = (i / NC) % RPW, c = i % NC;
+            const int row = (p0 + kk * nwaves) * RPW + r;
+            if (row < nrows) store(c, row, stash[i]);
+        }
+        k = 0;
+    };
+    // Windows of up to STASH_PASSES passes, three at a time; the stores of a window's totals come after
+    // its loop and are waited for before the next window's, which therefore starts with no store pending.
+    for (int p = wave;;) {
+        const int p0 = p;
+        bool done = false;
+        for (int it = 0; it < STASH_PASSES / 3; ++it) {
+            dma(slot2, p + 2 * nwaves);
+            pass(slot0, p);
+            if ((p += nwaves) >= npass) { done = true; break; }
+            dma(slot0, p + 2 * nwaves);
+            pass(slot1, p);
+            if ((p += nwaves) >= npass) { done = true; break; }
+            dma(slot1, p + 2 * nwaves);
+            pass(slot2, p);
+            if ((p += nwaves) >= npass) { done = true; break; }
+        }
+        flush(p0);
+        // also the end of the fills past the last pass, which must not outlive the wave
+        __builtin_amdgcn_s_waitcnt(0);
+        if (done) return;
+    }
+}
+
 // Streams rows [0, nrows) of one weight matrix (nb super-blocks per row, row_stride bytes apart) against
 // the NC columns staged in LDS; this wave takes passes wave, wave + nwaves, ... of 64/LPR rows each.
 // store(c, row, value) receives every row total of column c (called by one lane per row and column).
