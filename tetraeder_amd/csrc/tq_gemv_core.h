@@ -430,27 +430,30 @@ __device__ __forceinline__ void gemv_rows_m(const uint8_t *const (&ws)[M], int n
 
 // The same stream for a matrix of contiguous rows whose row bytes are a multiple of 16, through LDS: a
 // wave pass (64 / LPR whole rows, at most GEMV_DMA_SLOT bytes) goes global -> LDS in 1 KB wave loads
-// (buffer_load_dwordx4 ... lds, non-temporal) into one of three slots private to the wave, two passes
+// (buffer_load_dwordx4 ... lds, non-temporal) into one of NS slots private to the wave, NS - 1 passes
 // ahead of the one being computed, and every lane then reads its items from the slot. Each cache line
 // of the matrix is fetched by one wave load and no register holds data in flight. A wave reads only
-// what it loaded itself: no barrier, only its own load counter. The slots are three distinct LDS arrays
-// (the loop is unrolled three times), so the compiler waits for the one fill a read needs and not for
-// the two behind it; for that it must know how many loads were issued after it, so every fill issues
-// the same four wave loads, branch-free, and lanes past the pass (or fills past the last pass) take an
-// offset beyond the buffer's range, which loads nothing. (Buffer loads, not global ones: the compiler
-// makes every LDS read after a global_load_lds wait for all loads in flight.)
+// what it loaded itself: no barrier, only its own load counter: every fill issues the same four wave
+// loads, branch-free (lanes past the pass, and fills past the last pass, take an offset beyond the
+// buffer's range, which loads nothing), so a pass's fill is complete once at most the 4 (NS - 1) loads
+// of the fills issued after it are in flight, and the pass waits for exactly that. The slots are
+// distinct LDS arrays and the loop is unrolled NS times, so that every slot address is a constant.
+// (Buffer loads, not global ones: the compiler makes every LDS read after a global_load_lds wait for
+// all loads in flight.)
 constexpr int GEMV_DMA_SLOT = 4096;
-constexpr int WAIT_VMCNT_8 = 0x0F78;  // s_waitcnt vmcnt(8): expcnt and lgkmcnt at their maxima (no wait)
 constexpr int GEMV_DMA_STASH = 256;  // floats of row totals per wave
 
-template <int F, int NC, int LPR, class Stage, class Store>
-__device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int nb, int wave, int nwaves, uint8_t *slot0,
-                                              uint8_t *slot1, uint8_t *slot2, float *stash, const uint8_t *lds_qs,
+template <int F, int NC, int LPR, int NS, class Stage, class Store>
+__device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int nb, int wave, int nwaves,
+                                              uint8_t *const (&slots)[NS], float *stash, const uint8_t *lds_qs,
                                               const int16_t *lds_bs, const float *lds_d, Stage stage, Store store) {
+    static_assert(NS >= 2 && 4 * (NS - 1) < 16, "slots");
     constexpr int G = LPR / LPB;   // super-blocks of a row per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     constexpr int BYTES = FmtInfo<F>::bytes;
     static_assert(GEMV_DMA_SLOT / (RPW * BYTES) <= 2 * G, "a row that fits a slot has at most two items per lane");
+    // s_waitcnt vmcnt(4 (NS - 1)), expcnt and lgkmcnt at their maxima (no wait)
+    constexpr int WAIT_FILL = 0x0F70 | (4 * (NS - 1));
     const int lane = lane_id();
     const int u = lane % LPB, gb = (lane % LPR) / LPB, lrow = lane / LPR, lir = lane % LPR;
     const int npass = (nrows + RPW - 1) / RPW, BPL = (nb + G - 1) / G;
@@ -468,27 +471,24 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
     };
     const bool active = wave < npass;  // uniform over the wave
     if (active) {
-        dma(slot0, wave);
-        dma(slot1, wave + nwaves);
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) dma(slots[s], wave + s * nwaves);
     }
     stage();
     if (!active) return;
     // Row totals wait in the wave's stash until it is full or the stream ends: a store among the loads
     // would make the compiler wait for every load in flight (it cannot order the two kinds of access).
     constexpr int STASH_PASSES = GEMV_DMA_STASH / (RPW * NC);
-    static_assert(STASH_PASSES >= 3, "stash of at least one unrolled step");
+    static_assert(STASH_PASSES >= NS, "stash of at least one unrolled step");
     int k = 0;
     auto pass = [&](const uint8_t *slot, int p) {
-        // this pass's fill is complete once at most the two fills issued after it are in flight (the
-        // compiler's own count of LDS fills is not trusted across the loop's back edge)
-        __builtin_amdgcn_s_waitcnt(WAIT_VMCNT_8);
+        __builtin_amdgcn_s_waitcnt(WAIT_FILL);
         asm volatile("" ::: "memory");
         Acc<NC> acc;
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
         const int row = p * RPW + lrow;
-        // a pass fits one slot, so a row has at most 2 * G super-blocks: straight-line items keep each LDS
-        // read's address a fixed offset from its slot, which lets the compiler wait for that slot's DMA only
+        // a pass fits one slot, so a row has at most 2 * G super-blocks
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             if (j >= BPL) break;
@@ -515,21 +515,21 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
         }
         k = 0;
     };
-    // Windows of up to STASH_PASSES passes, three at a time; the stores of a window's totals come after
-    // its loop and are waited for before the next window's, which therefore starts with no store pending.
+    // Windows of up to STASH_PASSES passes, NS at a time; the stores of a window's totals come after its
+    // loop and are waited for before the next window's, which therefore starts with no store pending.
     for (int p = wave;;) {
         const int p0 = p;
         bool done = false;
-        for (int it = 0; it < STASH_PASSES / 3; ++it) {
-            dma(slot2, p + 2 * nwaves);
-            pass(slot0, p);
-            if ((p += nwaves) >= npass) { done = true; break; }
-            dma(slot0, p + 2 * nwaves);
-            pass(slot1, p);
-            if ((p += nwaves) >= npass) { done = true; break; }
-            dma(slot1, p + 2 * nwaves);
-            pass(slot2, p);
-            if ((p += nwaves) >= npass) { done = true; break; }
+        for (int it = 0; it < STASH_PASSES / NS && !done; ++it) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                dma(slots[(s + NS - 1) % NS], p + (NS - 1) * nwaves);
+                pass(slots[s], p);
+                if ((p += nwaves) >= npass) {
+                    done = true;
+                    break;
+                }
+            }
         }
         flush(p0);
         // also the end of the fills past the last pass, which must not outlive the wave
