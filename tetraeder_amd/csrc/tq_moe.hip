@@ -114,6 +114,7 @@ template <class Fn> __device__ __forceinline__ void moe_column_passes(int cnt, F
         const int n = min(MOE_NC, cnt - c0);
         if (n == 1) fn(NCT<1>(), c0, n);
         else if (n == 2) fn(NCT<2>(), c0, n);
+        else if (n == 3) fn(NCT<3>(), c0, n);
         else fn(NCT<MOE_NC>(), c0, n);
     }
 }
@@ -121,13 +122,12 @@ template <class Fn> __device__ __forceinline__ void moe_column_passes(int cnt, F
 __device__ __forceinline__ float moe_silu(float x) { return x / (1.0f + expf(-x)); }
 
 // Work weight of an expert with cnt columns, in proportion to the GEMV core's instructions per item:
-// the column passes of MOE_NC, each padded to 1, 2 or MOE_NC columns, cost 5 + 2 per extra column (on
-// MI355X a 3-token expert, padded to 4, streamed its rows 2.2 times slower than a 1-token expert).
+// the column passes of up to MOE_NC columns cost 5 + 2 per extra column (on MI355X a 3-token expert,
+// then padded to 4 columns, streamed its rows 2.2 times slower than a 1-token expert).
 __device__ __forceinline__ int moe_cost(int cnt) {
     int c = 0;
     for (int c0 = 0; c0 < cnt; c0 += MOE_NC) {
-        const int n = min(MOE_NC, cnt - c0), pad = n == 1 ? 1 : n == 2 ? 2 : MOE_NC;
-        c += 5 + 2 * (pad - 1);
+        c += 5 + 2 * (min(MOE_NC, cnt - c0) - 1);
     }
     return c;
 }
