@@ -352,6 +352,22 @@ def bench_secondary(ggml, torch, dev):
                                      "op_GBps": round(wb / op_us / 1e3, 1)}
     log(f"q4_K 4096x4096: {res['q4_K_gemv_4096x4096_m1']}")
     del W, ws
+    # the same kernels at a bandwidth-bound size: Q4_K 151936 x 2048 at batch 1 (175 MB, two copies
+    # alternated) and the Q6_K head at batch 4, kernel alone (activations already Q8_K)
+    for label, tyb, k, n, m in (("q4_K", ggml.Type.Q4_K, 2048, 151936, 1), ("q6_K", ggml.Type.Q6_K, 2048, 151936, 4)):
+        W = make_weights(ggml, torch, tyb, k, n, 2, seed=5 + m, dev=dev)
+        x = torch.randn((m, k), device=dev)
+        out = torch.empty((m, n), device=dev)
+        xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
+        wb = n * tyb.row_size(k)
+        kern_us = min(time_launches(torch, lambda i: ggml.mul_mat(W[i & 1], xq, out=out), 200),
+                      time_graph(torch, lambda i: ggml.mul_mat(W[i & 1], xq, out=out), 32))
+        key = f"{label}_gemv_{n}x{k}_m{m}"
+        res[key] = {"gemv_kernel_us": round(kern_us, 2), "gemv_GBps": round(wb / kern_us / 1e3, 1),
+                    "gemv_frac": round(wb / kern_us / 1e3 / PEAK_GBS, 4)}
+        log(f"{key}: {res[key]}")
+        del W
+    torch.cuda.empty_cache()
     # attention projections (Q4_K), decode batch 1, 4, 16, 32; 16 rotated layer copies
     shapes = (("q", 2048, 4096), ("k", 2048, 512), ("v", 2048, 512), ("o", 4096, 2048))
     copies = 16

@@ -433,10 +433,10 @@ __device__ __forceinline__ void gemv_rows_m(const uint8_t *const (&ws)[M], int n
 // (buffer_load_dwordx4 ... lds, non-temporal) into one of NS slots private to the wave, NS - 1 passes
 // ahead of the one being computed, and every lane then reads its items from the slot. Each cache line
 // of the matrix is fetched by one wave load and no register holds data in flight. A wave reads only
-// what it loaded itself: no barrier, only its own load counter: every fill issues the same four wave
-// loads, branch-free (lanes past the pass, and fills past the last pass, take an offset beyond the
-// buffer's range, which loads nothing), so a pass's fill is complete once at most the 4 (NS - 1) loads
-// of the fills issued after it are in flight, and the pass waits for exactly that. The slots are
+// what it loaded itself: no barrier, only its own load counter: every fill issues the same
+// GEMV_DMA_SLOT / 1 KB wave loads, branch-free (lanes past the pass, and fills past the last pass, take
+// an offset beyond the buffer's range, which loads nothing), so a pass's fill is complete once at most
+// the loads of the NS - 1 fills issued after it are in flight, and the pass waits for exactly that. The slots are
 // distinct LDS arrays and the loop is unrolled NS times, so that every slot address is a constant.
 // (Buffer loads, not global ones: the compiler makes every LDS read after a global_load_lds wait for
 // all loads in flight.)
@@ -447,13 +447,17 @@ template <int F, int NC, int LPR, int NS, class Stage, class Store>
 __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int nb, int wave, int nwaves,
                                               uint8_t *const (&slots)[NS], float *stash, const uint8_t *lds_qs,
                                               const int16_t *lds_bs, const float *lds_d, Stage stage, Store store) {
-    static_assert(NS >= 2 && 4 * (NS - 1) < 16, "slots");
+    constexpr int FILL = GEMV_DMA_SLOT / 1024;  // wave loads per slot fill
+    static_assert(GEMV_DMA_SLOT % 1024 == 0 && NS >= 2 && FILL * (NS - 1) < 64, "slots");
     constexpr int G = LPR / LPB;   // super-blocks of a row per wave pass
     constexpr int RPW = 64 / LPR;  // rows per wave pass
     constexpr int BYTES = FmtInfo<F>::bytes;
-    static_assert(GEMV_DMA_SLOT / (RPW * BYTES) <= 2 * G, "a row that fits a slot has at most two items per lane");
-    // s_waitcnt vmcnt(4 (NS - 1)), expcnt and lgkmcnt at their maxima (no wait)
-    constexpr int WAIT_FILL = 0x0F70 | (4 * (NS - 1));
+    // items per lane and pass at most (a pass fits one slot)
+    constexpr int BPL_MAX = (GEMV_DMA_SLOT / (RPW * BYTES) + G - 1) / G;
+    // s_waitcnt vmcnt(FILL (NS - 1)) (the count's low 4 bits at 3:0, its high 2 at 15:14), expcnt and
+    // lgkmcnt at their maxima (no wait)
+    constexpr int VM = FILL * (NS - 1);
+    constexpr int WAIT_FILL = (VM & 15) | ((VM >> 4) << 14) | 0x0F70;
     const int lane = lane_id();
     const int u = lane % LPB, gb = (lane % LPR) / LPB, lrow = lane / LPR, lir = lane % LPR;
     const int npass = (nrows + RPW - 1) / RPW, BPL = (nb + G - 1) / G;
@@ -463,7 +467,7 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
         const bool real = p < npass;
         const uint32_t start = real ? (uint32_t)p * span : 0u, len = real ? min(span, total - start) : 0u;
 #pragma unroll
-        for (int c = 0; c < GEMV_DMA_SLOT / 1024; ++c) {
+        for (int c = 0; c < FILL; ++c) {
             const uint32_t off = 1024 * c + 16 * lane;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(slot + 1024 * c), 16,
                                                      off < len ? start + off : total, 0, 0, 2 /* non-temporal */);
@@ -488,9 +492,8 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc.v[c] = 0.f;
         const int row = p * RPW + lrow;
-        // a pass fits one slot, so a row has at most 2 * G super-blocks
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < BPL_MAX; ++j) {
             if (j >= BPL) break;
             const int b = gb + j * G;
             Item<F> it;
