@@ -240,7 +240,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                      "traffic_over_algorithmic": traffic_ratio,
-                     "kernel": "k_gemv<q6_K,1 col>", "kernel_us": round(kern_us, 2)},
+                     "kernel": "k_gemv_dma<q6_K,1 col>", "kernel_us": round(kern_us, 2)},
         "cpu_baseline": cpu,
         "moe_mul_mat_id_us_per_token": {t: v["us_per_token"] for t, v in moe.items()},
         "secondary": secondary,
