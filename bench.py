@@ -266,7 +266,8 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
     """The MoE expert FFN step (gate, up, swiglu, down) at Qwen3-30B-A3B shapes: 128 experts, n_embd
     2048, n_ff 768, gate/up Q4_K, down Q6_K, top-8 with 10% -1. Steps rotate over `layers` weight copies
     (4 x 392 MB) and `routings` seeded id sets, captured in a HIP graph; the roofline bytes are the
-    unique valid experts of each step's ids."""
+    unique valid experts of each step's ids. us_per_step_summed: the same step through sum_experts
+    (moe_ffn_sum, [n_embd, T] out)."""
     n_embd, n_ff, E = 2048, 768, 128
     L = []
     for l in range(layers):
@@ -285,9 +286,14 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
         n = layers * routings
         step = lambda i: ggml.moe_ffn(*L[i % layers], x, ids[(i // layers) % routings], out=out, workspace=ws)  # noqa
         us = time_graph(torch, step, n)
+        # the same step through sum_experts (moe_ffn: the slots summed in the same launch)
+        out_sum = torch.empty((T, n_embd), device=dev)
+        step_sum = lambda i: ggml.moe_ffn_sum(*L[i % layers], x, ids[(i // layers) % routings], out=out_sum,  # noqa
+                                              workspace=ws)
+        us_sum = time_graph(torch, step_sum, n)
         mean_bytes = sum(uniq[(i // layers) % routings] for i in range(n)) / n * MOE_EXPERT_BYTES
         gbs = mean_bytes / us / 1e3
-        res[str(T)] = {"us_per_step": round(us, 2), "us_per_token": round(us / T, 2),
+        res[str(T)] = {"us_per_step": round(us, 2), "us_per_step_summed": round(us_sum, 2), "us_per_token": round(us / T, 2),
                        "unique_experts": round(mean_bytes / MOE_EXPERT_BYTES, 2),
                        "weight_MB": round(mean_bytes / 1e6, 2), "GBps": round(gbs, 1),
                        "frac": round(gbs / PEAK_GBS, 4)}

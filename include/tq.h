@@ -112,7 +112,7 @@ size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, con
 int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
                   size_t workspace_size, void *stream);
 
-/* Workspace bytes tq_moe_ffn needs for these operands. */
+/* Workspace bytes tq_moe_ffn and tq_moe_ffn_sum need for these operands. */
 size_t tq_moe_ffn_workspace_size(const tq_tensor *gate_exps, const tq_tensor *b, const tq_tensor *ids);
 
 /* The MoE expert FFN of one layer, the node sequence of weighted_experts
@@ -122,13 +122,28 @@ size_t tq_moe_ffn_workspace_size(const tq_tensor *gate_exps, const tq_tensor *b,
  * with gate_exps/up_exps [n_embd, n_ff, n_expert], down_exps [n_ff, n_embd, n_expert] (Q4_K or Q6_K
  * each), b F32 [n_embd, 1, T], ids I32 [n_used, T], weights F32 [1, n_used, T] or NULL (no scaling),
  * dst F32 [n_embd, n_used, T]. Slots with id < 0 read no weights and get exact zero rows. act is
- * quantized to Q8_K as the down MUL_MAT_ID would. Up to 256 slots (n_used * T) the whole step is two
- * launches (gate and up together; then swiglu, the Q8_K pass and down fused in one kernel); above that
- * the nodes run as separate MUL_MAT_ID launches with device routing. The sum over slots (sum_experts,
- * qwen3moe.rs:2917-2923) stays with the caller. */
+ * quantized to Q8_K as the down MUL_MAT_ID would. Up to 256 slots (n_used * T) the whole step is one
+ * launch (gate and up streamed together, swiglu, the Q8_K pass and down in the same kernel, its
+ * workgroups ordered by device counters; two launches where the GPU cannot hold a workgroup per routed
+ * expert); above that the nodes run as separate MUL_MAT_ID launches with device routing. The sum over
+ * slots (sum_experts, qwen3moe.rs:2917-2923) stays with the caller; tq_moe_ffn_sum includes it. */
 int tq_moe_ffn(const tq_tensor *gate_exps, const tq_tensor *up_exps, const tq_tensor *down_exps, const tq_tensor *b,
                const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
                void *stream);
+
+/* The MoE FFN of one layer through sum_experts: moe_ffn (crates/model/src/qwen3moe.rs:2892-2895) =
+ * sum_experts(weighted_experts(...)), the slots of each token added in choice order like the chain of
+ * ADD nodes of sum_experts (qwen3moe.rs:2917-2923). Operands as for tq_moe_ffn, dst F32 [n_embd, T]
+ * with contiguous rows. The per-slot rows go to the workspace and their sums follow in one more
+ * launch. */
+int tq_moe_ffn_sum(const tq_tensor *gate_exps, const tq_tensor *up_exps, const tq_tensor *down_exps,
+                   const tq_tensor *b, const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace,
+                   size_t workspace_size, void *stream);
+
+/* sum_experts (crates/model/src/qwen3moe.rs:2917-2923) on its own: experts F32 [n_embd, n_used, T]
+ * (contiguous rows, any slot and token strides) -> dst F32 [n_embd, T], dst[:, t] = experts[:, 0, t] +
+ * experts[:, 1, t] + ... added left to right in fp32. */
+int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream);
 
 /* Failed cross-workgroup waits of the single-launch MoE step (tq_moe_ffn up to 256 slots) on the current
  * device since the last clear: *count gets the error word (0: none), clear != 0 resets it. The step's

@@ -172,6 +172,17 @@ def mul_mat_id(ty: int, w: np.ndarray, k: int, n: int, n_expert: int, b: np.ndar
     return dst
 
 
+def sum_experts(experts: np.ndarray) -> np.ndarray:
+    """sum_experts (crates/model/src/qwen3moe.rs:2917-2923): float32 [T][n_used][n_embd] -> [T][n_embd]
+    by the reference's chain of ADD nodes over the choice views, view(0) + view(1), then + view(2), ...,
+    each an fp32 add."""
+    e = np.asarray(experts, dtype=np.float32)
+    acc = e[:, 0, :].copy()
+    for j in range(1, e.shape[1]):
+        acc = (acc + e[:, j, :]).astype(np.float32)
+    return acc
+
+
 def ref_f64(ty: int, w_rows: np.ndarray, k: int, x: np.ndarray):
     """(y, bound): f64 dot of dequantized rows with the Q8_K round trip of x, and 1e-5*sum|wx|+1e-6."""
     w_rows = np.ascontiguousarray(w_rows, dtype=np.uint8)

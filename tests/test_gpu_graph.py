@@ -78,9 +78,9 @@ def test_mul_mat_prefill_in_graph(gpu, tname, k, n, m):
 
 @pytest.mark.parametrize("tokens", [1, 16])
 def test_mul_mat_id_and_moe_ffn_in_graph(gpu, tokens):
-    """MUL_MAT_ID with device routing and the one-launch MoE step (phase-1 completion counts and the
-    exit count live on the device and are reset by the call's last workgroup), Qwen3-30B-A3B shapes,
-    10% of the ids -1."""
+    """MUL_MAT_ID with device routing and the one-launch MoE step, per slot and summed over the slots
+    (the step's phase-1 completion counts and exit count live on the device and are reset by the
+    call's last workgroup), Qwen3-30B-A3B shapes, 10% of the ids -1."""
     _case(f"moe tokens={tokens}")
     n_embd, n_ff, E = 2048, 768, 128
     gate = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=51, device=gpu)
@@ -95,12 +95,14 @@ def test_mul_mat_id_and_moe_ffn_in_graph(gpu, tokens):
     out_ffn = torch.empty((tokens, 8, n_embd), device=gpu)
     ws_ffn = torch.empty(max(1, ggml.moe_ffn_workspace_size(gate, x, ids)), dtype=torch.uint8, device=gpu)
     out_noise = torch.empty((tokens, 8, n_embd), device=gpu)
+    out_sum = torch.empty((tokens, n_embd), device=gpu)
 
     def op():
         ggml.mul_mat_id(gate, x, ids, out=out_id, workspace=ws_id)
         ggml.moe_ffn(gate, up, down, x, ids, rw, out=out_ffn, workspace=ws_ffn)
+        ggml.moe_ffn_sum(gate, up, down, x, ids, rw, out=out_sum, workspace=ws_ffn)
 
     # the noise runs the same step on other ids: the device counters must be back at zero after it
-    _check_replays(op, [out_id, out_ffn],
+    _check_replays(op, [out_id, out_ffn, out_sum],
                    lambda: ggml.moe_ffn(gate, up, down, x, ids2, rw, out=out_noise, workspace=ws_ffn))
     assert ggml.moe_sync_errors(clear=True) == 0

@@ -129,3 +129,48 @@ def test_moe_ffn_back_to_back_calls(gpu):
         assert bool((fused[ids < 0] == 0).all())
         worst = float((fused - ref).abs().max() / ref.abs().max())
         assert worst <= 3e-3, worst
+
+
+def test_sum_experts_matches_oracle(gpu):
+    """sum_experts on its own (qwen3moe.rs:2917-2923): bit-equal to the oracle's left-to-right fp32 fold,
+    also on a strided view (every other slot of a wider tensor)."""
+    _case("sum_experts")
+    rng = np.random.default_rng(11)
+    e = rng.standard_normal((6, 8, 2048)).astype(np.float32)
+    got = ggml.sum_experts(torch.from_numpy(e).to(gpu)).cpu().numpy()
+    np.testing.assert_array_equal(got, O.sum_experts(e))
+    wide = torch.from_numpy(rng.standard_normal((3, 16, 2048)).astype(np.float32)).to(gpu)
+    view = wide[:, ::2, :]
+    got = ggml.sum_experts(view).cpu().numpy()
+    np.testing.assert_array_equal(got, O.sum_experts(view.cpu().numpy()))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 4, 16, 32, 40])
+def test_moe_ffn_sum(gpu, tokens):
+    """moe_ffn (qwen3moe.rs:2892-2895) = sum_experts(weighted_experts): the summed step equals the
+    oracle's fold of the per-slot step's rows bit for bit (the slot rows are the same arithmetic); 40
+    tokens (320 slots) runs the composed path and a sum launch. No wait ran out."""
+    _case(f"moe_ffn_sum tokens={tokens}")
+    n_embd, n_ff, E = 2048, 768, 128
+    gate = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=41, device=gpu)
+    up = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=42, device=gpu)
+    down = make_experts(ggml.Type.Q6_K, n_ff, n_embd, E, seed=43, device=gpu)
+    ids = torch.from_numpy(qwen3_moe_ids(tokens, seed=900 + tokens)).to(gpu)
+    x = torch.from_numpy(normal((tokens, 1, n_embd), 950 + tokens)).to(gpu)
+    w = torch.from_numpy(np.random.default_rng(tokens).random((tokens, 8, 1)).astype(np.float32)).to(gpu)
+    ggml.moe_sync_errors(clear=True)
+    slots = ggml.moe_ffn(gate, up, down, x, ids, w)
+    out = torch.full((tokens, n_embd), float("nan"), device=gpu)
+    ggml.moe_ffn_sum(gate, up, down, x, ids, w, out=out)
+    torch.cuda.synchronize()
+    assert ggml.moe_sync_errors() == 0
+    np.testing.assert_array_equal(out.cpu().numpy(), O.sum_experts(slots.cpu().numpy()))
+    # again with every slot of one token skipped (-1): its sum is an exact zero row
+    ids2 = ids.clone()
+    ids2[0, :] = -1
+    out2 = ggml.moe_ffn_sum(gate, up, down, x, ids2, w)
+    slots2 = ggml.moe_ffn(gate, up, down, x, ids2, w)
+    torch.cuda.synchronize()
+    assert ggml.moe_sync_errors() == 0
+    np.testing.assert_array_equal(out2.cpu().numpy(), O.sum_experts(slots2.cpu().numpy()))
+    assert bool((out2[0] == 0).all())

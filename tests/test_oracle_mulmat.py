@@ -116,3 +116,17 @@ def test_mul_mat_id_matches_per_expert_mul_mat(ty, tokens, b1):
     np.testing.assert_array_equal(got, want)
     neg = ids < 0
     assert np.all(got[neg] == 0.0) and np.all(np.signbit(got[neg]) == 0)
+
+
+def test_sum_experts_adds_left_to_right():
+    """sum_experts (crates/model/src/qwen3moe.rs:2917-2923) folds the choice views with fp32 adds from
+    the first: (1e8 + 1) - 1e8 is 0 in fp32 (1e8 + 1 rounds to 1e8), where a sum from the right or in
+    float64 gives 1; a single choice is returned as is."""
+    e = np.array([[[1e8], [1.0], [-1e8]]], dtype=np.float32)
+    assert O.sum_experts(e)[0, 0] == np.float32(0.0)
+    assert np.float64(1e8) + 1.0 - 1e8 == 1.0
+    one = np.array([[[3.5, -2.0]]], dtype=np.float32)
+    np.testing.assert_array_equal(O.sum_experts(one), one[:, 0, :])
+    rng = np.random.default_rng(3)
+    r = rng.standard_normal((5, 8, 64)).astype(np.float32)
+    np.testing.assert_allclose(O.sum_experts(r), r.astype(np.float64).sum(axis=1), rtol=0, atol=1e-5)

@@ -440,9 +440,35 @@ static size_t moe_workspace(const tq_tensor *gate, const tq_tensor *b, const tq_
     return bytes;
 }
 
+// tq_moe_ffn_sum keeps the slot rows [n_slots][n_embd] after what tq_moe_ffn needs
+static size_t moe_sum_workspace(const tq_tensor *gate, const tq_tensor *b, const tq_tensor *ids) {
+    const int64_t n_slots = ids->ne[0] * ids->ne[1], n_embd = gate->ne[0];
+    return moe_workspace(gate, b, ids) + align_up((size_t)n_slots * n_embd * 4, 256);
+}
+
 size_t tq_moe_ffn_workspace_size(const tq_tensor *gate, const tq_tensor *b, const tq_tensor *ids) {
     if (!gate || !b || !ids) return 0;
-    return moe_workspace(gate, b, ids);
+    return moe_sum_workspace(gate, b, ids);
+}
+
+// The single-launch step's arguments for checked operands (dst: the slot rows [n_embd, n_used, T]).
+static MoeArgs moe_args(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
+                        const tq_tensor *ids, const tq_tensor *weights, const tq_tensor *dst, float *gu) {
+    MoeArgs m{};
+    m.gate = (const uint8_t *)gate->data, m.up = (const uint8_t *)up->data, m.down = (const uint8_t *)down->data;
+    m.g_s1 = (int64_t)gate->nb[1], m.g_s2 = (int64_t)gate->nb[2];
+    m.u_s1 = (int64_t)up->nb[1], m.u_s2 = (int64_t)up->nb[2];
+    m.dn_s1 = (int64_t)down->nb[1], m.dn_s2 = (int64_t)down->nb[2];
+    m.n_embd = (int32_t)gate->ne[0], m.n_ff = (int32_t)gate->ne[1], m.n_expert = (int32_t)gate->ne[2];
+    m.n_used = (int32_t)ids->ne[0], m.ntok = (int32_t)ids->ne[1];
+    m.ids = (const uint8_t *)ids->data, m.ids_s0 = (int64_t)ids->nb[0], m.ids_s1 = (int64_t)ids->nb[1];
+    m.b = (const float *)b->data, m.b_s2 = (int64_t)(b->nb[2] / 4);
+    m.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[2] % 16 == 0;
+    if (weights) m.rw = (const float *)weights->data, m.rw_s1 = (int64_t)(weights->nb[1] / 4),
+                 m.rw_s2 = (int64_t)(weights->nb[2] / 4);
+    m.gu = gu;
+    m.dst = (float *)dst->data, m.o_s1 = (int64_t)(dst->nb[1] / 4), m.o_s2 = (int64_t)(dst->nb[2] / 4);
+    return m;
 }
 
 int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
@@ -462,20 +488,7 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
     hipStream_t s = (hipStream_t)stream;
     float *gu = (float *)ws;
     if (n_slots <= mmid_small_max_slots()) {
-        MoeArgs m{};
-        m.gate = (const uint8_t *)gate->data, m.up = (const uint8_t *)up->data, m.down = (const uint8_t *)down->data;
-        m.g_s1 = (int64_t)gate->nb[1], m.g_s2 = (int64_t)gate->nb[2];
-        m.u_s1 = (int64_t)up->nb[1], m.u_s2 = (int64_t)up->nb[2];
-        m.dn_s1 = (int64_t)down->nb[1], m.dn_s2 = (int64_t)down->nb[2];
-        m.n_embd = (int32_t)n_embd, m.n_ff = (int32_t)n_ff, m.n_expert = (int32_t)gate->ne[2];
-        m.n_used = (int32_t)n_used, m.ntok = (int32_t)T;
-        m.ids = (const uint8_t *)ids->data, m.ids_s0 = (int64_t)ids->nb[0], m.ids_s1 = (int64_t)ids->nb[1];
-        m.b = (const float *)b->data, m.b_s2 = (int64_t)(b->nb[2] / 4);
-        m.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[2] % 16 == 0;
-        if (weights) m.rw = (const float *)weights->data, m.rw_s1 = (int64_t)(weights->nb[1] / 4),
-                     m.rw_s2 = (int64_t)(weights->nb[2] / 4);
-        m.gu = gu;
-        m.dst = (float *)dst->data, m.o_s1 = (int64_t)(dst->nb[1] / 4), m.o_s2 = (int64_t)(dst->nb[2] / 4);
+        const MoeArgs m = moe_args(gate, up, down, b, ids, weights, dst, gu);
         if (moe_fused_supported(gate->type, up->type, m))
             return check_hip(launch_moe_fused(gate->type, down->type, m, 0, s), "moe_ffn launch");
         return check_hip(launch_moe_ffn(gate->type, up->type, down->type, m, s), "moe_ffn launch");
@@ -499,6 +512,57 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
                                            (int64_t)(dst->nb[1] / 4), (int64_t)(dst->nb[2] / 4), s),
                          "scale_rows launch");
     return TQ_STATUS_SUCCESS;
+}
+
+int tq_moe_ffn_sum(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
+                   const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
+                   void *stream) {
+    int rc;
+    if (!gate || !up || !down || !b || !ids || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor");
+    if ((rc = check_tensor(dst, "dst")) || (rc = check_f32(dst, "dst"))) return rc;
+    if ((rc = check_tensor(gate, "gate")) || (rc = check_tensor(ids, "ids"))) return rc;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], n_slots = n_used * T, n_embd = gate->ne[0];
+    if (dst->ne[0] != n_embd || dst->ne[1] != T || dst->ne[2] != 1 || dst->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "dst shape is not [n_embd, T]");
+    if (dst->nb[0] != 4) return fail(TQ_STATUS_FAILED, "dst rows must be contiguous");
+    if (n_slots == 0) return TQ_STATUS_SUCCESS;
+    const size_t need = moe_sum_workspace(gate, b, ids), base = moe_workspace(gate, b, ids);
+    if (workspace && workspace_size < need)
+        return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
+    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+    if (!ws) return rc;
+    // the slot rows as a contiguous [n_embd, n_used, T] tensor in the workspace
+    tq_tensor so{};
+    so.type = TQ_TYPE_F32, so.data = ws + base;
+    so.ne[0] = n_embd, so.ne[1] = n_used, so.ne[2] = T, so.ne[3] = 1;
+    so.nb[0] = 4, so.nb[1] = (size_t)n_embd * 4, so.nb[2] = so.nb[1] * n_used, so.nb[3] = so.nb[2] * T;
+    if ((rc = check_moe(gate, up, down, b, ids, weights, &so))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    // the slot rows, then their sums in a launch of its own (a grid-wide wait at the end of the
+    // single-launch step cost 8-18 us more than the second launch's 3.4)
+    if ((rc = tq_moe_ffn(gate, up, down, b, ids, weights, &so, ws, base, stream))) return rc;
+    return check_hip(launch_sum_experts((const float *)so.data, n_embd, (int)n_used, T, n_embd, n_embd * n_used,
+                                        (float *)dst->data, (int64_t)(dst->nb[1] / 4), s),
+                     "sum_experts launch");
+}
+
+int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream) {
+    int rc;
+    if (!experts || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor");
+    if ((rc = check_tensor(experts, "experts")) || (rc = check_f32(experts, "experts")) || (rc = check_tensor(dst, "dst")) ||
+        (rc = check_f32(dst, "dst")))
+        return rc;
+    const int64_t n_embd = experts->ne[0], n_used = experts->ne[1], T = experts->ne[2];
+    if (experts->ne[3] != 1 || n_used < 1 || n_used > 0x7fffffff)
+        return fail(TQ_STATUS_FAILED, "experts must be [n_embd, n_used, T]");
+    if (dst->ne[0] != n_embd || dst->ne[1] != T || dst->ne[2] != 1 || dst->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "dst shape is not [n_embd, T]");
+    if (experts->nb[0] != 4 || dst->nb[0] != 4) return fail(TQ_STATUS_FAILED, "rows must be contiguous");
+    if (experts->nb[1] % 4 || experts->nb[2] % 4 || dst->nb[1] % 4) return fail(TQ_STATUS_FAILED, "unaligned strides");
+    return check_hip(launch_sum_experts((const float *)experts->data, n_embd, (int)n_used, T, (int64_t)(experts->nb[1] / 4),
+                                        (int64_t)(experts->nb[2] / 4), (float *)dst->data, (int64_t)(dst->nb[1] / 4),
+                                        (hipStream_t)stream),
+                     "sum_experts launch");
 }
 
 int tq_moe_ffn_sync_errors(unsigned *count, int clear) {

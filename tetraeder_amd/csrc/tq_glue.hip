@@ -1,8 +1,11 @@
 // tq_glue.hip -- the elementwise step glue around MUL_MAT_ID in the MoE expert FFN for large token
-// counts (crates/model/src/qwen3moe.rs:2909-2913): act = swiglu_split(gate, up) = silu(gate) * up, and the
-// multiply of expert outputs by the router weights.
+// counts (crates/model/src/qwen3moe.rs:2909-2913): act = swiglu_split(gate, up) = silu(gate) * up, the
+// multiply of expert outputs by the router weights, and sum_experts (qwen3moe.rs:2917-2923), the sum
+// over the selected experts in choice order.
 #include "tq_device.h"
 #include "tq_internal.h"
+
+#include <algorithm>
 
 namespace tq {
 
@@ -25,6 +28,28 @@ __global__ __launch_bounds__(256) void k_scale_rows(float *__restrict__ x, int64
     float *row = x + j * x_s1 + t * x_s2;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < row_len; i += (int64_t)gridDim.x * blockDim.x)
         row[i] *= s;
+}
+
+// out[e, t] = x[e, 0, t] + x[e, 1, t] + ... + x[e, n_used - 1, t], added left to right in fp32 like the
+// reference's chain of ADD nodes over the views of each choice
+__global__ __launch_bounds__(256) void k_sum_experts(const float *__restrict__ x, int64_t n_embd, int n_used,
+                                                     int64_t x_s1, int64_t x_s2, float *__restrict__ out,
+                                                     int64_t o_s1) {
+    const int64_t t = blockIdx.y;
+    const float *xt = x + t * x_s2;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_embd; e += (int64_t)gridDim.x * blockDim.x) {
+        float acc = xt[e];
+        for (int j = 1; j < n_used; ++j) acc += xt[j * x_s1 + e];
+        out[t * o_s1 + e] = acc;
+    }
+}
+
+hipError_t launch_sum_experts(const float *x, int64_t n_embd, int n_used, int64_t ntok, int64_t x_s1, int64_t x_s2,
+                              float *out, int64_t o_s1, hipStream_t stream) {
+    if (ntok == 0 || n_embd == 0) return hipSuccess;
+    const unsigned bx = (unsigned)std::min<int64_t>((n_embd + 255) / 256, 64);
+    k_sum_experts<<<dim3(bx, (unsigned)ntok), 256, 0, stream>>>(x, n_embd, n_used, x_s1, x_s2, out, o_s1);
+    return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const float *gate, const float *up, float *out, int64_t n, hipStream_t stream) {

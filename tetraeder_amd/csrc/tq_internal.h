@@ -126,6 +126,8 @@ hipError_t launch_moe_fused(int type_gate, int type_down, const MoeArgs &m, unsi
 // Failed waits recorded by the fused MoE launches on the current device since the last clear.
 hipError_t moe_sync_errors(unsigned *out, bool clear);
 hipError_t launch_swiglu(const float *gate, const float *up, float *out, int64_t n, hipStream_t stream);
+hipError_t launch_sum_experts(const float *x, int64_t n_embd, int n_used, int64_t ntok, int64_t x_s1, int64_t x_s2,
+                              float *out, int64_t o_s1, hipStream_t stream);
 hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
                              int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream);
 

@@ -224,6 +224,41 @@ def moe_ffn(gate: QTensor, up: QTensor, down: QTensor, b: torch.Tensor, ids: tor
     return out
 
 
+def moe_ffn_sum(gate: QTensor, up: QTensor, down: QTensor, b: torch.Tensor, ids: torch.Tensor,
+                weights: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """moe_ffn (crates/model/src/qwen3moe.rs:2892-2895): the expert FFN above summed over each token's
+    slots in choice order (sum_experts, qwen3moe.rs:2917-2923). Operands as for moe_ffn; returns
+    [T, n_embd]."""
+    if b.dtype != torch.float32 or ids.dtype != torch.int32 or b.dim() != 3 or ids.dim() != 2:
+        raise Invalid("b is float32 [T, 1, n_embd] and ids int32 [T, n_used]")
+    T = ids.shape[0]
+    if out is None:
+        out = torch.empty((T, gate.ne[0]), dtype=torch.float32, device=b.device)
+    gt, ut, dt_, bt, it, ot = gate.raw(), up.raw(), down.raw(), _dense(b, Type.F32), _dense(ids, Type.I32), \
+        _dense(out, Type.F32)
+    wt = C.byref(_dense(weights, Type.F32)) if weights is not None else None
+    ws_ptr, ws_size = 0, 0
+    if workspace is not None:
+        ws_ptr, ws_size = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    _check(_lib.lib().tq_moe_ffn_sum(C.byref(gt), C.byref(ut), C.byref(dt_), C.byref(bt), C.byref(it), wt,
+                                     C.byref(ot), ws_ptr, ws_size, _stream(stream)))
+    return out
+
+
+def sum_experts(experts: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """sum_experts (crates/model/src/qwen3moe.rs:2917-2923): float32 [T, n_used, n_embd] -> [T, n_embd],
+    each token's slots added left to right."""
+    if experts.dtype != torch.float32 or experts.dim() != 3:
+        raise Invalid("experts is float32 [T, n_used, n_embd]")
+    T, _, n_embd = experts.shape
+    if out is None:
+        out = torch.empty((T, n_embd), dtype=torch.float32, device=experts.device)
+    et, ot = _dense(experts, Type.F32), _dense(out, Type.F32)
+    _check(_lib.lib().tq_sum_experts(C.byref(et), C.byref(ot), _stream(stream)))
+    return out
+
+
 def moe_sync_errors(clear: bool = False) -> int:
     """Failed cross-workgroup waits of the single-launch MoE step on the current device (0: none)."""
     v = C.c_uint(0)
