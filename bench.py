@@ -267,7 +267,7 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
     2048, n_ff 768, gate/up Q4_K, down Q6_K, top-8 with 10% -1. Steps rotate over `layers` weight copies
     (4 x 392 MB) and `routings` seeded id sets, captured in a HIP graph; the roofline bytes are the
     unique valid experts of each step's ids. us_per_step_summed: the same step through sum_experts
-    (moe_ffn_sum, [n_embd, T] out)."""
+    (moe_ffn_sum, [n_embd, T] out); router_us: the router ahead of it (moe_router)."""
     n_embd, n_ff, E = 2048, 768, 128
     L = []
     for l in range(layers):
@@ -297,6 +297,13 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
                        "unique_experts": round(mean_bytes / MOE_EXPERT_BYTES, 2),
                        "weight_MB": round(mean_bytes / 1e6, 2), "GBps": round(gbs, 1),
                        "frac": round(gbs / PEAK_GBS, 4)}
+        # the router ahead of the step (rms_norm, the F32 gate_inp logits, softmax, top-8, weights)
+        gate_inp = torch.randn((E, n_embd), device=dev) * 0.02
+        norm = torch.ones(n_embd, device=dev)
+        x2 = x.view(T, n_embd)
+        wsr = torch.empty(max(1, ggml.moe_router_workspace_size(gate_inp, x2)), dtype=torch.uint8, device=dev)
+        res[str(T)]["router_us"] = round(time_graph(torch, lambda i: ggml.moe_router(x2, norm, gate_inp, 1e-6, 8,
+                                                                                      workspace=wsr), 16), 2)
         log(f"moe T={T}: {res[str(T)]}")
     del L
     torch.cuda.empty_cache()

@@ -145,6 +145,20 @@ int tq_moe_ffn_sum(const tq_tensor *gate_exps, const tq_tensor *up_exps, const t
  * experts[:, 1, t] + ... added left to right in fp32. */
 int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream);
 
+/* Workspace bytes tq_moe_router needs (the logits, n_expert * T floats). */
+size_t tq_moe_router_workspace_size(const tq_tensor *gate_inp, const tq_tensor *ffn_inp);
+
+/* The MoE router of one layer, `router` (crates/model/src/qwen3moe.rs:2869-2887): xn = rms_norm(ffn_inp,
+ * eps) * ffn_norm; probs = soft_max(MUL_MAT(gate_inp, xn)); ids = argsort_top_k(probs, n_used) (largest
+ * first; equal probabilities: the lower expert id first); weights = probs[ids] / clamp(sum, 2^-14, inf).
+ * ffn_inp F32 [n_embd, T] (n_embd <= 8192, T <= 65535) and ffn_norm F32 [n_embd], gate_inp F32
+ * [n_embd, n_expert] (n_expert <= 1024), 1 <= n_used <= min(n_expert, 64); outputs xn F32 [n_embd, T], weights F32 [1, n_used, T] and ids I32
+ * [n_used, T], ready for tq_moe_ffn / tq_moe_ffn_sum on the same stream (nothing leaves the device). The
+ * squares of rms_norm and the exponentials of soft_max are summed in double, as ggml's CPU ops do. */
+int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_tensor *gate_inp, float eps, int n_used,
+                  tq_tensor *xn, tq_tensor *weights, tq_tensor *ids, void *workspace, size_t workspace_size,
+                  void *stream);
+
 /* Failed cross-workgroup waits of the single-launch MoE step (tq_moe_ffn up to 256 slots) on the current
  * device since the last clear: *count gets the error word (0: none), clear != 0 resets it. The step's
  * workgroups wait for each other with bounded polls; a wait that runs out (only possible when the GPU

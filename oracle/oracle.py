@@ -183,6 +183,40 @@ def sum_experts(experts: np.ndarray) -> np.ndarray:
     return acc
 
 
+def router(x: np.ndarray, norm: np.ndarray, gate: np.ndarray, eps: float, n_used: int):
+    """The MoE router (crates/model/src/qwen3moe.rs:2869-2887) on float32 x [T][n_embd], norm [n_embd]
+    and gate [n_expert][n_embd], with ggml's CPU arithmetic for each node: rms_norm sums the float32
+    squares in double (mean = sum / n as float32, scale = 1 / sqrtf(mean + eps)); the logits (MUL_MAT)
+    here are float64 dots rounded to float32 (ggml's SIMD order is another fp32 rounding of the same
+    sum); soft_max subtracts the max, sums the float32 exponentials in double and scales by
+    (float)(1 / sum); argsort_top_k keeps the n_used largest, largest first, equal values by the lower
+    id (crates/ggml-sys/tests/ggml.rs:33-44 fixes the order on [0.1, 0.9, 0.3, 0.5]: ids [1, 3]);
+    get_rows, sum_rows (double), clamp(sum, 2^-14, inf) and div. Returns (xn, probs, weights, ids)."""
+    x = np.asarray(x, dtype=np.float32)
+    norm = np.asarray(norm, dtype=np.float32)
+    gate = np.asarray(gate, dtype=np.float32)
+    n = x.shape[1]
+    ss = (x * x).astype(np.float64).sum(axis=1)
+    mean = (ss / n).astype(np.float32)
+    scale = (np.float32(1.0) / np.sqrt(mean + np.float32(eps), dtype=np.float32)).astype(np.float32)
+    xn = ((x * scale[:, None]).astype(np.float32) * norm).astype(np.float32)
+    logits = (xn.astype(np.float64) @ gate.astype(np.float64).T).astype(np.float32)
+    mx = logits.max(axis=1, keepdims=True)
+    e = np.exp((logits - mx).astype(np.float32)).astype(np.float32)
+    inv = (1.0 / e.astype(np.float64).sum(axis=1)).astype(np.float32)
+    probs = (e * inv[:, None]).astype(np.float32)
+    T, E = probs.shape
+    ids = np.zeros((T, n_used), dtype=np.int32)
+    for t in range(T):
+        order = sorted(range(E), key=lambda i: (-float(probs[t, i]), i))
+        ids[t] = order[:n_used]
+    sel = np.take_along_axis(probs, ids.astype(np.int64), axis=1)
+    ssum = sel.astype(np.float64).sum(axis=1).astype(np.float32)
+    div = np.maximum(ssum, np.float32(6.103515625e-5))
+    w = (sel / div[:, None]).astype(np.float32)
+    return xn, probs, w, ids
+
+
 def ref_f64(ty: int, w_rows: np.ndarray, k: int, x: np.ndarray):
     """(y, bound): f64 dot of dequantized rows with the Q8_K round trip of x, and 1e-5*sum|wx|+1e-6."""
     w_rows = np.ascontiguousarray(w_rows, dtype=np.uint8)

@@ -130,3 +130,24 @@ def test_sum_experts_adds_left_to_right():
     rng = np.random.default_rng(3)
     r = rng.standard_normal((5, 8, 64)).astype(np.float32)
     np.testing.assert_allclose(O.sum_experts(r), r.astype(np.float64).sum(axis=1), rtol=0, atol=1e-5)
+
+
+def test_router_top_k_order_and_weights():
+    """The reference's own top-k case (crates/ggml-sys/tests/ggml.rs:33-44: scores [0.1, 0.9, 0.3, 0.5],
+    k = 2 -> ids [1, 3]) through the router with one embedding dimension (a one-weight gate row per
+    expert makes the logits the scores times xn > 0); the weights are the selected probabilities over
+    their sum; rms_norm of a constant row is sign(x) / sqrt(1 + eps / x^2) times the norm weight; a
+    probability tie goes to the lower id."""
+    x = np.array([[2.0]], dtype=np.float32)
+    gate = np.array([[0.1], [0.9], [0.3], [0.5]], dtype=np.float32)
+    xn, probs, w, ids = O.router(x, np.ones(1, np.float32), gate, 1e-6, 2)
+    assert ids.tolist() == [[1, 3]]
+    np.testing.assert_allclose(probs.sum(axis=1), 1.0, rtol=1e-6)
+    sel = probs[0, [1, 3]]
+    np.testing.assert_allclose(w[0], sel / sel.sum(), rtol=1e-6)
+    np.testing.assert_allclose(xn[0, 0], 2.0 / np.sqrt(4.0 + 1e-6), rtol=1e-6)
+    c = np.full((1, 8), -3.0, np.float32)
+    xn, _, _, _ = O.router(c, np.full(8, 0.5, np.float32), np.ones((2, 8), np.float32), 0.0, 1)
+    np.testing.assert_allclose(xn, -0.5, rtol=1e-6)
+    _, _, _, ids = O.router(np.ones((1, 4), np.float32), np.ones(4, np.float32), np.ones((3, 4), np.float32), 1e-6, 2)
+    assert ids.tolist() == [[0, 1]]

@@ -570,6 +570,59 @@ int tq_moe_ffn_sync_errors(unsigned *count, int clear) {
     return check_hip(moe_sync_errors(count, clear != 0), "moe sync error read");
 }
 
+size_t tq_moe_router_workspace_size(const tq_tensor *gate_inp, const tq_tensor *ffn_inp) {
+    if (!gate_inp || !ffn_inp) return 0;
+    return align_up((size_t)gate_inp->ne[1] * (size_t)ffn_inp->ne[1] * 4, 256);
+}
+
+int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_tensor *gate_inp, float eps, int n_used,
+                  tq_tensor *xn, tq_tensor *weights, tq_tensor *ids, void *workspace, size_t workspace_size,
+                  void *stream) {
+    int rc;
+    if ((rc = check_tensor(ffn_inp, "ffn_inp")) || (rc = check_f32(ffn_inp, "ffn_inp")) ||
+        (rc = check_tensor(ffn_norm, "ffn_norm")) || (rc = check_f32(ffn_norm, "ffn_norm")) ||
+        (rc = check_tensor(gate_inp, "gate_inp")) || (rc = check_f32(gate_inp, "gate_inp")) ||
+        (rc = check_tensor(xn, "xn")) || (rc = check_f32(xn, "xn")) || (rc = check_tensor(weights, "weights")) ||
+        (rc = check_f32(weights, "weights")) || (rc = check_tensor(ids, "ids")))
+        return rc;
+    const int64_t n_embd = ffn_inp->ne[0], T = ffn_inp->ne[1], n_expert = gate_inp->ne[1];
+    if (ffn_inp->ne[2] != 1 || ffn_inp->ne[3] != 1) return fail(TQ_STATUS_FAILED, "ffn_inp must be [n_embd, T]");
+    if (ffn_norm->ne[0] != n_embd || ffn_norm->ne[1] != 1) return fail(TQ_STATUS_FAILED, "ffn_norm must be [n_embd]");
+    if (gate_inp->ne[0] != n_embd || gate_inp->ne[2] != 1 || gate_inp->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "gate_inp must be F32 [n_embd, n_expert]");
+    if (n_embd < 1 || n_embd > ROUTER_MAX_EMBD)
+        return fail(TQ_STATUS_FAILED, "n_embd = %lld is outside 1..%d", (long long)n_embd, ROUTER_MAX_EMBD);
+    if (n_expert < 1 || n_expert > ROUTER_MAX_EXPERTS)
+        return fail(TQ_STATUS_FAILED, "n_expert = %lld is outside 1..%d", (long long)n_expert, ROUTER_MAX_EXPERTS);
+    if (n_used < 1 || n_used > n_expert || n_used > ROUTER_MAX_USED)
+        return fail(TQ_STATUS_FAILED, "n_used = %d is outside 1..min(n_expert, %d)", n_used, ROUTER_MAX_USED);
+    if (T > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 tokens");
+    if (xn->ne[0] != n_embd || xn->ne[1] != T || xn->ne[2] != 1 || xn->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "xn shape is not [n_embd, T]");
+    if (weights->ne[0] != 1 || weights->ne[1] != n_used || weights->ne[2] != T || weights->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "weights shape is not [1, n_used, T]");
+    if (ids->type != TQ_TYPE_I32 || ids->ne[0] != n_used || ids->ne[1] != T || ids->ne[2] != 1 || ids->ne[3] != 1 ||
+        ids->nb[0] % 4 || ids->nb[1] % 4 || (uintptr_t)ids->data % 4)
+        return fail(TQ_STATUS_FAILED, "ids must be I32 [n_used, T]");
+    if (T == 0) return TQ_STATUS_SUCCESS;
+    const size_t need = tq_moe_router_workspace_size(gate_inp, ffn_inp);
+    if (workspace && workspace_size < need)
+        return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
+    float *ws = (float *)(workspace ? workspace : own_workspace(need, &rc));
+    if (!ws) return rc;
+    RouterArgs a{};
+    a.x = (const float *)ffn_inp->data, a.x_s1 = (int64_t)(ffn_inp->nb[1] / 4);
+    a.norm = (const float *)ffn_norm->data;
+    a.gate = (const float *)gate_inp->data, a.g_s1 = (int64_t)(gate_inp->nb[1] / 4);
+    a.eps = eps;
+    a.n_embd = (int32_t)n_embd, a.n_expert = (int32_t)n_expert, a.n_used = n_used, a.ntok = (int32_t)T;
+    a.xn = (float *)xn->data, a.xn_s1 = (int64_t)(xn->nb[1] / 4);
+    a.logits = ws;
+    a.ids = (int32_t *)ids->data, a.ids_s0 = (int64_t)(ids->nb[0] / 4), a.ids_s1 = (int64_t)(ids->nb[1] / 4);
+    a.w = (float *)weights->data, a.w_s1 = (int64_t)(weights->nb[1] / 4), a.w_s2 = (int64_t)(weights->nb[2] / 4);
+    return check_hip(launch_router(a, (hipStream_t)stream), "router launch");
+}
+
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {
     if (!is_weight(type) && type != TQ_TYPE_Q8_K) return fail(TQ_STATUS_FAILED, "to_f32: type %d", type);
     if (n % QK) return fail(TQ_STATUS_FAILED, "to_f32: n = %lld is not a multiple of 256", (long long)n);

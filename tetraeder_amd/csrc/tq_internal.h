@@ -131,6 +131,27 @@ hipError_t launch_sum_experts(const float *x, int64_t n_embd, int n_used, int64_
 hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
                              int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream);
 
+// The MoE router (rms_norm, gate_inp logits, softmax, top-k, normalized weights) for T tokens.
+constexpr int ROUTER_MAX_EXPERTS = 1024, ROUTER_MAX_USED = 64;
+constexpr int ROUTER_MAX_EMBD = 8192;  // the token's normalized row is held in LDS (32 KiB)
+struct RouterArgs {
+    const float *x;       // ffn_inp, token t at x + t*x_s1 (n_embd floats)
+    int64_t x_s1;
+    const float *norm;    // ffn_norm, n_embd floats
+    const float *gate;    // gate_inp F32, expert e's row at gate + e*g_s1 (n_embd floats)
+    int64_t g_s1;
+    float eps;
+    int32_t n_embd, n_expert, n_used, ntok;
+    float *xn;            // xn of token t at xn + t*xn_s1
+    int64_t xn_s1;
+    float *logits;        // workspace, [T][n_expert]
+    int32_t *ids;         // id j of token t at ids[j*ids_s0 + t*ids_s1]
+    int64_t ids_s0, ids_s1;
+    float *w;             // weight j of token t at w[j*w_s1 + t*w_s2]
+    int64_t w_s1, w_s2;
+};
+hipError_t launch_router(const RouterArgs &a, hipStream_t stream);
+
 // Device properties cached per device.
 int device_cu_count();
 // Waves of a kernel one CU holds at once (register and LDS limits), for sizing streaming grids.

@@ -259,6 +259,36 @@ def sum_experts(experts: torch.Tensor, out: torch.Tensor | None = None, stream=N
     return out
 
 
+def moe_router(ffn_inp: torch.Tensor, ffn_norm: torch.Tensor, gate_inp: torch.Tensor, eps: float, n_used: int,
+               workspace: torch.Tensor | None = None, stream=None):
+    """The MoE router (crates/model/src/qwen3moe.rs:2869-2887): ffn_inp float32 [T, n_embd], ffn_norm
+    [n_embd], gate_inp float32 [n_expert, n_embd] (ggml's [n_embd, n_expert]) -> (xn [T, n_embd],
+    weights [T, n_used, 1], ids int32 [T, n_used]), as moe_ffn takes them."""
+    for t, nm in ((ffn_inp, "ffn_inp"), (ffn_norm, "ffn_norm"), (gate_inp, "gate_inp")):
+        if t.dtype != torch.float32:
+            raise Invalid(f"{nm} must be float32")
+    if ffn_inp.dim() != 2 or ffn_norm.dim() != 1 or gate_inp.dim() != 2:
+        raise Invalid("ffn_inp is [T, n_embd], ffn_norm [n_embd], gate_inp [n_expert, n_embd]")
+    T, n_embd = ffn_inp.shape
+    dev = ffn_inp.device
+    xn = torch.empty((T, n_embd), dtype=torch.float32, device=dev)
+    w = torch.empty((T, n_used, 1), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, n_used), dtype=torch.int32, device=dev)
+    xt, nt, gt = _dense(ffn_inp, Type.F32), _dense(ffn_norm, Type.F32), _dense(gate_inp, Type.F32)
+    ot, wt, it = _dense(xn, Type.F32), _dense(w, Type.F32), _dense(ids, Type.I32)
+    ws_ptr, ws_size = 0, 0
+    if workspace is not None:
+        ws_ptr, ws_size = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    _check(_lib.lib().tq_moe_router(C.byref(xt), C.byref(nt), C.byref(gt), eps, n_used, C.byref(ot), C.byref(wt),
+                                    C.byref(it), ws_ptr, ws_size, _stream(stream)))
+    return xn, w, ids
+
+
+def moe_router_workspace_size(gate_inp: torch.Tensor, ffn_inp: torch.Tensor) -> int:
+    gt, xt = _dense(gate_inp, Type.F32), _dense(ffn_inp, Type.F32)
+    return int(_lib.lib().tq_moe_router_workspace_size(C.byref(gt), C.byref(xt)))
+
+
 def moe_sync_errors(clear: bool = False) -> int:
     """Failed cross-workgroup waits of the single-launch MoE step on the current device (0: none)."""
     v = C.c_uint(0)
