@@ -7,7 +7,8 @@ roofline: the GEMV kernel alone (activation already Q8_K), timed with HIP events
 launched on, algorithmic bytes = weight bytes per launch.
 cpu_baseline: the restated iqk AVX-512 VNNI CPU path (oracle/tq_cpu_baseline.c) on the host cores,
 same weight bytes, Q8_K quantization included, median of calls within a bounded budget.
-secondary: the other workloads (Q4_K GEMV 4096 x 4096 batch 1, attention projections, MoE step).
+secondary: the other workloads (Q4_K GEMV 4096 x 4096 batch 1, attention projections, MoE step and
+router, prefill, expert slot uploads from host memory).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -40,7 +41,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--moe-tokens", type=int, default=0, help="with --only moe: run just this token count")
-    p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill", "secondary"], default=None,
+    p.add_argument("--only", choices=["gemv", "copy", "moe", "prefill", "secondary", "slots"], default=None,
                    help="profiling runs: 'gemv' launches only the headline GEMV kernel (--steps times), "
                         "'copy' a plain 256 MiB device copy (--steps times) to scale the HBM byte counters")
     return p.parse_args()
@@ -153,6 +154,9 @@ def main():
     if args.only == "secondary":
         print(json.dumps(bench_secondary(ggml, torch, dev)))
         return
+    if args.only == "slots":
+        print(json.dumps(bench_slots(ggml, torch, dev)))
+        return
     if args.only == "prefill":
         print(json.dumps(bench_prefill(ggml, torch, dev, only=os.environ.get("TQ_BENCH_PROFILE") == "1")))
         return
@@ -229,6 +233,7 @@ def main():
         secondary["moe_step"] = moe
         secondary.update(bench_secondary(ggml, torch, dev))
         secondary["prefill"] = bench_prefill(ggml, torch, dev)
+        secondary["expert_slot_upload"] = bench_slots(ggml, torch, dev, moe)
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -307,6 +312,36 @@ def bench_moe(ggml, torch, np, dev, layers=4, routings=8, tokens=None):
         log(f"moe T={T}: {res[str(T)]}")
     del L
     torch.cuda.empty_cache()
+    return res
+
+
+def bench_slots(ggml, torch, dev, moe=None):
+    """Expert slot uploads (copy_expert_slots) at Qwen3-30B-A3B shapes: the 8 experts of a decode token
+    (3,059,712 B each: the gate, up and down slabs) from pinned host memory into 8 device slots, on the
+    kernel engine (workgroups reading host memory over PCIe) and on the copy engines (one
+    hipMemcpyAsync per slab, as ggml_backend_tensor_set issues them), set against the same experts in
+    HBM: their share of the measured 1-token step and their bytes at the 8 TB/s peak."""
+    n_embd, n_ff, n_host, n_dev = 2048, 768, 16, 8
+    host, slots = [], []
+    for ty, k, n in ((ggml.Type.Q4_K, n_embd, n_ff), (ggml.Type.Q4_K, n_embd, n_ff), (ggml.Type.Q6_K, n_ff, n_embd)):
+        slab = ty.row_size(k) * n
+        buf = torch.empty(slab * n_host, dtype=torch.uint8, pin_memory=True)
+        buf.copy_(torch.randint(0, 256, (slab * n_host,), dtype=torch.uint8))
+        host.append(ggml.QTensor(ty, (k, n, n_host), buf))
+        slots.append(ggml.QTensor(ty, (k, n, n_dev), torch.empty(slab * n_dev, dtype=torch.uint8, device=dev)))
+    res = {"experts_per_call": n_dev, "bytes_per_call": n_dev * MOE_EXPERT_BYTES}
+    for name, engine in (("kernel", ggml.COPY_KERNEL), ("dma", ggml.COPY_DMA)):
+        def call(i, engine=engine):
+            first = (i % 2) * n_dev  # alternate between the two halves of the host slots
+            ggml.copy_expert_slots(host, slots, range(first, first + n_dev), range(n_dev), engine=engine)
+        us = time_launches(torch, call, 20)
+        res[name] = {"us_per_call": round(us, 1), "us_per_expert": round(us / n_dev, 2),
+                     "GBps": round(n_dev * MOE_EXPERT_BYTES / us / 1e3, 2)}
+    res["hbm_peak_us_per_expert"] = round(MOE_EXPERT_BYTES / PEAK_GBS / 1e3, 3)
+    if moe and "1" in moe:
+        res["step_us_per_expert_T1"] = round(moe["1"]["us_per_step"] / moe["1"]["unique_experts"], 2)
+    log(f"slots: {res}")
+    del host, slots
     return res
 
 

@@ -159,6 +159,24 @@ int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_
                   tq_tensor *xn, tq_tensor *weights, tq_tensor *ids, void *workspace, size_t workspace_size,
                   void *stream);
 
+/* Engines of tq_copy_expert_slots. */
+enum {
+    TQ_COPY_AUTO = 0,   /* the kernel where its conditions hold, else the copy engines */
+    TQ_COPY_KERNEL = 1, /* one launch whose workgroups read pinned host memory over PCIe */
+    TQ_COPY_DMA = 2,    /* one hipMemcpyAsync per slab: the copy engines, no CU time (pageable sources too) */
+};
+
+/* Makes experts resident in device slots: for copy i and tensor p < n_tensors (gate, up, down), the raw
+ * slab of host slot from[i] of src[p] goes to device slot to[i] of dst[p], asynchronously on stream
+ * (the host bytes are read when the stream gets there). Replaces copy_slot
+ * (crates/model/src/experts.rs:1880-1893), one ggml_backend_tensor_set per slab
+ * (crates/ggml-sys/src/ggml/context.rs:651-664), for all slabs of n experts at once. src[p] and dst[p]
+ * are [K, N, n_slots] with equal type, ne[0], ne[1], nb[0] and nb[1]; the slab is ne[1] * nb[1] bytes
+ * at slot stride nb[2]. src in host memory (pinned for TQ_COPY_KERNEL), dst in device memory;
+ * n_tensors 1..4; slots must exist and no device slot may be written twice by one call. */
+int tq_copy_expert_slots(const tq_tensor *src, const tq_tensor *dst, int n_tensors, const uint32_t *from,
+                         const uint32_t *to, int n, int engine, void *stream);
+
 /* Failed cross-workgroup waits of the single-launch MoE step (tq_moe_ffn up to 256 slots) on the current
  * device since the last clear: *count gets the error word (0: none), clear != 0 resets it. The step's
  * workgroups wait for each other with bounded polls; a wait that runs out (only possible when the GPU

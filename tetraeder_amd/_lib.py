@@ -38,6 +38,8 @@ _SIGNATURES = {
     "tq_moe_router_workspace_size": ([C.POINTER(TqTensor), C.POINTER(TqTensor)], C.c_size_t),
     "tq_moe_router": ([C.POINTER(TqTensor)] * 3 + [C.c_float, C.c_int] + [C.POINTER(TqTensor)] * 3 +
                       [C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "tq_copy_expert_slots": ([C.POINTER(TqTensor), C.POINTER(TqTensor), C.c_int, C.POINTER(C.c_uint32),
+                              C.POINTER(C.c_uint32), C.c_int, C.c_int, C.c_void_p], C.c_int),
     "tq_moe_ffn_sync_errors": ([C.POINTER(C.c_uint), C.c_int], C.c_int),
     "tq_to_f32": ([C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p], C.c_int),
     "tq_quantize_weights": ([C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p], C.c_int),

@@ -182,6 +182,41 @@ static size_t mul_mat_split_part(const tq_tensor *a, const tq_tensor *b) {
     return align_up(mmq_split_bytes(a->type, b->ne[1], a->ne[1], (int)(a->ne[0] / QK), (int)(b->ne[2] * b->ne[3])), 256);
 }
 
+// The device address through which a kernel reads [p, p + len) of pinned host memory, or NULL when
+// the range is not inside one host allocation known to HIP (pageable memory included). Failed
+// queries leave no error behind for the next launch check.
+static const uint8_t *pinned_device_address(const void *p, size_t len) {
+    hipPointerAttribute_t attr{};
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (attr.type != hipMemoryTypeHost || !attr.devicePointer) return nullptr;
+    // the allocation's extent, looked up by the address as given, else by its device address
+    const uint8_t *addr = (const uint8_t *)p;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+        (void)hipGetLastError();
+        addr = (const uint8_t *)attr.devicePointer;
+        if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)attr.devicePointer) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    if (addr < (const uint8_t *)base || addr + len > (const uint8_t *)base + size) return nullptr;
+    return (const uint8_t *)attr.devicePointer;
+}
+
+static bool is_device_memory(const void *p) {
+    hipPointerAttribute_t attr{};
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -621,6 +656,74 @@ int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_
     a.ids = (int32_t *)ids->data, a.ids_s0 = (int64_t)(ids->nb[0] / 4), a.ids_s1 = (int64_t)(ids->nb[1] / 4);
     a.w = (float *)weights->data, a.w_s1 = (int64_t)(weights->nb[1] / 4), a.w_s2 = (int64_t)(weights->nb[2] / 4);
     return check_hip(launch_router(a, (hipStream_t)stream), "router launch");
+}
+
+int tq_copy_expert_slots(const tq_tensor *src, const tq_tensor *dst, int n_tensors, const uint32_t *from,
+                         const uint32_t *to, int n, int engine, void *stream) {
+    if (!src || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor list");
+    if (n_tensors < 1 || n_tensors > SLOT_MAX_TENSORS)
+        return fail(TQ_STATUS_FAILED, "n_tensors = %d is outside 1..%d", n_tensors, SLOT_MAX_TENSORS);
+    if (n < 0 || (n > 0 && (!from || !to))) return fail(TQ_STATUS_FAILED, "copy list: n = %d, from/to NULL", n);
+    if (engine != TQ_COPY_AUTO && engine != TQ_COPY_KERNEL && engine != TQ_COPY_DMA)
+        return fail(TQ_STATUS_FAILED, "engine %d is not TQ_COPY_AUTO, TQ_COPY_KERNEL or TQ_COPY_DMA", engine);
+    int rc;
+    size_t slab[SLOT_MAX_TENSORS];
+    for (int p = 0; p < n_tensors; ++p) {
+        const tq_tensor *s = &src[p], *d = &dst[p];
+        if ((rc = check_tensor(s, "src")) || (rc = check_tensor(d, "dst"))) return rc;
+        if (s->type != d->type || s->ne[0] != d->ne[0] || s->ne[1] != d->ne[1] || s->nb[0] != d->nb[0] ||
+            s->nb[1] != d->nb[1] || s->ne[3] != 1 || d->ne[3] != 1)
+            return fail(TQ_STATUS_FAILED, "tensor %d: src and dst slots differ in type, rows or row layout", p);
+        slab[p] = (size_t)s->nb[1] * (size_t)s->ne[1];
+        if (s->nb[2] < slab[p] || d->nb[2] < slab[p])
+            return fail(TQ_STATUS_FAILED, "tensor %d: slots overlap (nb[2] below the slab's %zu bytes)", p, slab[p]);
+        if (n && !is_device_memory(d->data)) return fail(TQ_STATUS_FAILED, "tensor %d: dst is not device memory", p);
+    }
+    for (int i = 0; i < n; ++i) {
+        for (int p = 0; p < n_tensors; ++p)
+            if ((int64_t)from[i] >= src[p].ne[2] || (int64_t)to[i] >= dst[p].ne[2])
+                return fail(TQ_STATUS_FAILED, "copy %d: slot %u -> %u is outside %lld host / %lld device slots", i,
+                            from[i], to[i], (long long)src[p].ne[2], (long long)dst[p].ne[2]);
+        for (int j = 0; j < i; ++j)
+            if (to[j] == to[i]) return fail(TQ_STATUS_FAILED, "copies %d and %d both write device slot %u", j, i, to[i]);
+    }
+    if (n == 0) return TQ_STATUS_SUCCESS;
+    // the kernel engine: pinned sources covering every slot read, whole 16-byte words at 16-byte
+    // aligned addresses
+    const uint8_t *dev_src[SLOT_MAX_TENSORS] = {nullptr};
+    bool kernel_ok = true;
+    for (int p = 0; p < n_tensors && kernel_ok; ++p) {
+        uint32_t hi = 0;
+        for (int i = 0; i < n; ++i) hi = std::max(hi, from[i]);
+        dev_src[p] = pinned_device_address(src[p].data, (size_t)src[p].nb[2] * hi + slab[p]);
+        kernel_ok = dev_src[p] && slab[p] % 16 == 0 && (uintptr_t)dev_src[p] % 16 == 0 && src[p].nb[2] % 16 == 0 &&
+                    (uintptr_t)dst[p].data % 16 == 0 && dst[p].nb[2] % 16 == 0;
+    }
+    if (engine == TQ_COPY_KERNEL && !kernel_ok)
+        return fail(TQ_STATUS_FAILED, "TQ_COPY_KERNEL needs pinned host sources (hipHostMalloc) and 16-byte aligned "
+                                      "slabs of whole 16-byte words");
+    if (engine == TQ_COPY_DMA || !kernel_ok) {
+        for (int i = 0; i < n; ++i)
+            for (int p = 0; p < n_tensors; ++p) {
+                const uint8_t *s = (const uint8_t *)src[p].data + (size_t)src[p].nb[2] * from[i];
+                uint8_t *d = (uint8_t *)dst[p].data + (size_t)dst[p].nb[2] * to[i];
+                if ((rc = check_hip(hipMemcpyAsync(d, s, slab[p], hipMemcpyHostToDevice, (hipStream_t)stream),
+                                    "slot copy")))
+                    return rc;
+            }
+        return TQ_STATUS_SUCCESS;
+    }
+    for (int i0 = 0; i0 < n; i0 += SLOT_MAX_COPIES) {
+        SlotCopyArgs a{};
+        a.n_tensors = n_tensors, a.n = std::min(SLOT_MAX_COPIES, n - i0);
+        for (int p = 0; p < n_tensors; ++p) {
+            a.src[p] = dev_src[p], a.dst[p] = (uint8_t *)dst[p].data;
+            a.src_stride[p] = (int64_t)src[p].nb[2], a.dst_stride[p] = (int64_t)dst[p].nb[2], a.slab[p] = (int64_t)slab[p];
+        }
+        for (int i = 0; i < a.n; ++i) a.from[i] = from[i0 + i], a.to[i] = to[i0 + i];
+        if ((rc = check_hip(launch_copy_slots(a, (hipStream_t)stream), "slot copy launch"))) return rc;
+    }
+    return TQ_STATUS_SUCCESS;
 }
 
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {

@@ -131,6 +131,19 @@ hipError_t launch_sum_experts(const float *x, int64_t n_embd, int n_used, int64_
 hipError_t launch_scale_rows(float *x, int64_t row_len, int n_used, int64_t ntok, const float *w, int64_t w_s1,
                              int64_t w_s2, int64_t x_s1, int64_t x_s2, hipStream_t stream);
 
+// Expert slot uploads: copy i moves slab `from[i]` of every source tensor p (pinned host memory, read
+// through its device address) to slab `to[i]` of destination tensor p. Slabs are whole 16-byte words
+// at 16-byte aligned addresses; the destination slabs of a call do not overlap.
+constexpr int SLOT_MAX_TENSORS = 4, SLOT_MAX_COPIES = 256;
+struct SlotCopyArgs {
+    const uint8_t *src[SLOT_MAX_TENSORS];
+    uint8_t *dst[SLOT_MAX_TENSORS];
+    int64_t src_stride[SLOT_MAX_TENSORS], dst_stride[SLOT_MAX_TENSORS], slab[SLOT_MAX_TENSORS];
+    int n_tensors, n;
+    uint32_t from[SLOT_MAX_COPIES], to[SLOT_MAX_COPIES];
+};
+hipError_t launch_copy_slots(const SlotCopyArgs &a, hipStream_t stream);
+
 // The MoE router (rms_norm, gate_inp logits, softmax, top-k, normalized weights) for T tokens.
 constexpr int ROUTER_MAX_EXPERTS = 1024, ROUTER_MAX_USED = 64;
 constexpr int ROUTER_MAX_EMBD = 8192;  // the token's normalized row is held in LDS (32 KiB)

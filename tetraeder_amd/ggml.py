@@ -289,6 +289,35 @@ def moe_router_workspace_size(gate_inp: torch.Tensor, ffn_inp: torch.Tensor) -> 
     return int(_lib.lib().tq_moe_router_workspace_size(C.byref(gt), C.byref(xt)))
 
 
+COPY_AUTO, COPY_KERNEL, COPY_DMA = 0, 1, 2
+
+
+def copy_expert_slots(src: list, dst: list, from_slots, to_slots, engine: int = COPY_AUTO, stream=None) -> None:
+    """Makes experts resident in device slots: for every pair (from_slots[i], to_slots[i]) and every
+    tensor p, the raw slab of host slot from_slots[i] of src[p] goes to device slot to_slots[i] of dst[p]
+    (the device side of copy_slot, crates/model/src/experts.rs:1880-1893, for a batch of experts).
+    src: QTensors over host bytes (pinned for COPY_KERNEL: torch's pin_memory=True), dst: QTensors over
+    device bytes, [K, N, n_slots] with the same type and rows. Asynchronous on the stream: the host
+    bytes must not change until the stream has passed the copy."""
+    if len(src) != len(dst):
+        raise Invalid("src and dst list different tensor counts")
+    n = len(from_slots)
+    if len(to_slots) != n:
+        raise Invalid("from_slots and to_slots differ in length")
+    for t in src:
+        if t.data.is_cuda:
+            raise Invalid("src slabs must be in host memory")
+    for t in dst:
+        if not t.data.is_cuda:
+            raise Invalid("dst slots must be in device memory")
+    k = len(src)
+    srcs = (_lib.TqTensor * max(1, k))(*[t.raw() for t in src])
+    dsts = (_lib.TqTensor * max(1, k))(*[t.raw() for t in dst])
+    fr = (C.c_uint32 * max(1, n))(*[int(v) for v in from_slots])
+    to = (C.c_uint32 * max(1, n))(*[int(v) for v in to_slots])
+    _check(_lib.lib().tq_copy_expert_slots(srcs, dsts, k, fr, to, n, int(engine), _stream(stream)))
+
+
 def moe_sync_errors(clear: bool = False) -> int:
     """Failed cross-workgroup waits of the single-launch MoE step on the current device (0: none)."""
     v = C.c_uint(0)
