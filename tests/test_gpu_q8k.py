@@ -80,3 +80,25 @@ def test_q8_K_golden(gpu):
     g = np.load(GOLDEN)
     got = ggml.quantize_q8_K(torch.from_numpy(g["x"]).to(gpu)).cpu().numpy()
     np.testing.assert_array_equal(got, g["q8"])
+
+
+@pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
+@pytest.mark.parametrize("kind", ["normal", "ties", "zero_blocks", "dup_max", "extreme"])
+def test_in_kernel_quantization_matches_the_pass(gpu, tname, kind):
+    """Decode-size F32 activations are quantized by the GEMV workgroups into LDS (wave reductions by DPP
+    and permlane swaps); the GEMV over them equals, bit for bit, the GEMV over the same activations
+    quantized by the Q8_K pass (itself bit-identical to ggml's quantize_row_q8_K above)."""
+    from tests.test_gpu_gemv import make_weights
+    _case(f"in-kernel {tname} {kind}")
+    ty = ggml.Type.Q4_K if tname == "q4_K" else ggml.Type.Q6_K
+    k = 2048
+    w = make_weights(ty, k, 512, 1, seed=17, device=gpu)
+    for m in (1, 2):
+        x = torch.from_numpy(np.ascontiguousarray(_inputs(kind, m, k, 40 + m))).to(gpu)
+        assert ggml.mul_mat_workspace_size(w, x) == 0  # the in-kernel path
+        got = ggml.mul_mat(w, x)
+        xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
+        want = ggml.mul_mat(w, xq)
+        torch.cuda.synchronize()
+        assert got.numel() == want.numel() == m * 512
+        assert torch.equal(got.reshape(-1), want.reshape(-1)), f"m={m}: in-kernel Q8_K differs from the pass"

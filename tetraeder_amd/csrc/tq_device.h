@@ -84,6 +84,36 @@ template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
 }
 
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false); }
+
+template <int CTRL> __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    return ((uint64_t)dpp_u<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u<CTRL>((uint32_t)v);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// The other 16-lane row's (W = 16) or the other 32-lane half's (W = 32) copy of v.
+template <int W> __device__ __forceinline__ uint32_t swap_rows(uint32_t x) {
+    if constexpr (W == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return ((threadIdx.x >> 4) & 1) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return ((threadIdx.x >> 5) & 1) ? r[0] : r[1];
+    }
+}
+
+// The largest 64-bit key of the wave, in every lane: DPP within rows, permlane swaps across them.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
+    v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
+    v = max_u64(v, ((uint64_t)swap_rows<16>((uint32_t)(v >> 32)) << 32) | swap_rows<16>((uint32_t)v));
+    v = max_u64(v, ((uint64_t)swap_rows<32>((uint32_t)(v >> 32)) << 32) | swap_rows<32>((uint32_t)v));
+    return v;
+}
+
 template <int W> __device__ __forceinline__ float group_sum(float v) {
     static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
     if (W >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]

@@ -87,6 +87,9 @@ template <int F>
 __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], int cb, uint8_t *lds_qs, int16_t *lds_bs,
                                                           float *lds_d) {
     const int lane = lane_id();
+    // max = the first element of largest magnitude (ggml's strict '>' scan): the lane's own first, then
+    // the wave's largest key, |x| bits (non-negative floats order as their bits) above the complemented
+    // index, so equal magnitudes go to the lower index; DPP and permlane exchanges, no LDS round trips
     float amax = 0.f, vmax = 0.f;
     int imax = 0x7fffffff;
 #pragma unroll
@@ -94,17 +97,14 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
         const float x = fabsf(v[j]);
         if (x > amax) amax = x, vmax = v[j], imax = lane * 4 + j;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float a2 = __shfl_xor(amax, off, 64);
-        const float v2 = __shfl_xor(vmax, off, 64);
-        const int i2 = __shfl_xor(imax, off, 64);
-        if (a2 > amax || (a2 == amax && i2 < imax)) amax = a2, vmax = v2, imax = i2;
-    }
+    const uint64_t best = wave_max_u64(((uint64_t)__float_as_uint(amax) << 32) | (uint32_t)~imax);
+    amax = __uint_as_float(__builtin_amdgcn_readfirstlane((int)(uint32_t)(best >> 32)));
     uint32_t packed = 0;
     int sum = 0;
     float d = 0.f;
     if (amax != 0.f) {
+        const int owner = __builtin_amdgcn_readfirstlane((int)(~(uint32_t)best) >> 2);
+        vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vmax), owner));
         const float iscale = __fdiv_rn(-127.f, vmax);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -116,14 +116,19 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
         d = __fdiv_rn(1.f, iscale);
     }
     *(uint32_t *)(lds_qs + cb * ACT_QS_PITCH + act_perm<F>(4 * lane)) = packed;
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);  // lanes 4g..4g+3 hold the sum of 16-element group g
-    if (F == FMT_Q4K) sum += __shfl_xor(sum, 4, 64);  // lanes 8g..8g+7: the 32-element sum of 2g, 2g+1
-    constexpr int SLOTS = ActSlots<F>::n;
-    const int slot = lane < LPB * SLOTS ? lane : 0;
-    const int g = act_bs_src<F>(slot / SLOTS, slot % SLOTS);
-    const int bs = __shfl(sum, 4 * g, 64);
-    if (lane < LPB * SLOTS) lds_bs[cb * (ACT_BS_BYTES / 2) + lane] = (int16_t)bs;
+    // bsums: lanes 4k..4k+3 end with the sum of 16-element group k (Q4_K: lanes 8k..8k+7 with the
+    // 32-element sum of groups 2k, 2k+1), and the first lane of the group writes the slot that takes it
+    // (the inverse of act_bs_src)
+    sum += dpp_i<0xB1>(sum);  // quad_perm [1,0,3,2]
+    sum += dpp_i<0x4E>(sum);  // quad_perm [2,3,0,1]
+    int16_t *bs = lds_bs + cb * (ACT_BS_BYTES / 2);
+    if (F == FMT_Q4K) {
+        sum += dpp_i<0x141>(sum);  // row_half_mirror: the other quad of the 8 lanes
+        if ((lane & 7) == 0) bs[lane >> 3] = (int16_t)sum;
+    } else if ((lane & 3) == 0) {
+        const int k = lane >> 2, h = k >> 3, s = (k & 7) >> 1, vv = k & 1;
+        bs[(2 * h + vv) * ActSlots<F>::n + s] = (int16_t)sum;
+    }
     if (lane == 0) lds_d[cb] = d;
 }
 

@@ -305,6 +305,14 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
         bool ready = false;
         moe_column_passes(cnt, [&](auto nct, int c0, int n) {
             constexpr int NC = decltype(nct)::value;
+            // the pass's output offsets and router weights, loaded before the weight stream starts
+            int64_t my_off = 0;
+            float my_sc = 0.f;
+            if ((int)threadIdx.x < n && threadIdx.x < NC) {
+                const int sl = cols[c0 + threadIdx.x], j = sl % m.n_used, t = sl / m.n_used;
+                my_off = j * m.o_s1 + t * m.o_s2;
+                my_sc = m.rw ? m.rw[j * m.rw_s1 + t * m.rw_s2] : 1.f;
+            }
             auto stage = [&]() {
                 __syncthreads();  // every wave is done with the previous columns
                 if (!ready) {
@@ -336,16 +344,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
                     wave_quantize_vals_to_lds<FD>(v, kk * nb2 + blk, lds_qs, lds_bs, lds_d);
                 }
                 zero_columns<NC>(n, nb2, lds_qs, lds_bs, lds_d);
-                if (threadIdx.x < NC) {
-                    int64_t off = 0;
-                    float sc = 0.f;
-                    if ((int)threadIdx.x < n) {
-                        const int sl = cols[c0 + threadIdx.x], j = sl % m.n_used, t = sl / m.n_used;
-                        off = j * m.o_s1 + t * m.o_s2;
-                        sc = m.rw ? m.rw[j * m.rw_s1 + t * m.rw_s2] : 1.f;
-                    }
-                    col_off[threadIdx.x] = off, col_scale[threadIdx.x] = sc;
-                }
+                if (threadIdx.x < NC) col_off[threadIdx.x] = my_off, col_scale[threadIdx.x] = my_sc;
                 __syncthreads();
             };
             float *dst = m.dst + p0 * RPW2;

@@ -50,25 +50,6 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     return fmaxf(fmaxf(rd_f(v, 15), rd_f(v, 31)), fmaxf(rd_f(v, 47), rd_f(v, 63)));
 }
 
-template <int CTRL> __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {  // lanes with no source: their own
-    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    const uint32_t l2 = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, 0xf, 0xf, false);
-    const uint32_t h2 = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, 0xf, 0xf, false);
-    return ((uint64_t)h2 << 32) | l2;
-}
-__device__ __forceinline__ uint64_t rd_u64(uint64_t v, int l) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-}
-__device__ __forceinline__ uint64_t max_u64(uint64_t x, uint64_t y) { return x > y ? x : y; }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    v = max_u64(v, dpp_u64<0x111>(v));
-    v = max_u64(v, dpp_u64<0x112>(v));
-    v = max_u64(v, dpp_u64<0x114>(v));
-    v = max_u64(v, dpp_u64<0x118>(v));
-    return max_u64(max_u64(rd_u64(v, 15), rd_u64(v, 31)), max_u64(rd_u64(v, 47), rd_u64(v, 63)));
-}
-
 template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
     const int2 h = __builtin_bit_cast(int2, v);
     const int lo = __builtin_amdgcn_update_dpp(0, h.x, CTRL, 0xf, 0xf, false);
