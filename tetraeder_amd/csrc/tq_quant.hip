@@ -14,17 +14,19 @@ namespace tq {
 //   an all-zero block gets d = 0 and qs = 0 (bsums are written as 0 here; ggml leaves them).
 // The division is IEEE correctly rounded (__fdiv_rn) and the product is not fused into anything, so
 // the bytes equal the CPU's. The parallel argmax keeps the first occurrence: among equal |x| the
-// smaller element index wins, which is what the left-to-right strict > scan selects.
+// smaller element index wins, which is what the left-to-right strict > scan selects (one 64-bit
+// maximum over the wave by DPP and permlane exchanges).
 // ---------------------------------------------------------------------------------------------
-template <bool VEC>
-__global__ __launch_bounds__(256) void k_quantize_q8_K(const char *__restrict__ x, int64_t nbk, int64_t nblocks,
-                                                       int64_t ne1, int64_t ne2, size_t s1, size_t s2, size_t s3,
-                                                       uint8_t *__restrict__ y) {
-    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// I: the index type of the block arithmetic (32-bit divisions are a few instructions, 64-bit ones a
+// subroutine each).
+template <bool VEC, class I>
+__global__ __launch_bounds__(256) void k_quantize_q8_K(const char *__restrict__ x, I nbk, I nblocks, I ne1, I ne2,
+                                                       size_t s1, size_t s2, size_t s3, uint8_t *__restrict__ y) {
+    const I g = (I)blockIdx.x * 4 + (I)(threadIdx.x >> 6);
     if (g >= nblocks) return;
     const int lane = lane_id();
-    const int64_t r = g / nbk, blk = g - r * nbk;
-    const int64_t i1 = r % ne1, t = r / ne1, i2 = t % ne2, i3 = t / ne2;
+    const I r = g / nbk, blk = g - r * nbk;
+    const I i1 = r % ne1, t = r / ne1, i2 = t % ne2, i3 = t / ne2;
     const float *src = (const float *)(x + i1 * s1 + i2 * s2 + i3 * s3) + blk * QK + lane * 4;
     float v[4];
     if (VEC) {
@@ -41,18 +43,17 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const char *__restrict__ 
         const float a = fabsf(v[j]);
         if (a > amax) amax = a, vmax = v[j], imax = lane * 4 + j;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float a2 = __shfl_xor(amax, off, 64);
-        const float v2 = __shfl_xor(vmax, off, 64);
-        const int i2x = __shfl_xor(imax, off, 64);
-        if (a2 > amax || (a2 == amax && i2x < imax)) amax = a2, vmax = v2, imax = i2x;
-    }
-    uint8_t *blkp = y + g * Q8K_BYTES;
+    // the wave's largest key: |x| bits (non-negative floats order as their bits) above the complemented
+    // index, so equal magnitudes go to the lower index
+    const uint64_t best = wave_max_u64(((uint64_t)__float_as_uint(amax) << 32) | (uint32_t)~imax);
+    amax = __uint_as_float(__builtin_amdgcn_readfirstlane((int)(uint32_t)(best >> 32)));
+    uint8_t *blkp = y + (size_t)g * Q8K_BYTES;
     uint32_t packed = 0;
     int s = 0;
     float d = 0.f;
     if (amax != 0.f) {
+        const int owner = __builtin_amdgcn_readfirstlane((int)(~(uint32_t)best) >> 2);
+        vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vmax), owner));
         const float iscale = __fdiv_rn(-127.f, vmax);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -64,8 +65,8 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const char *__restrict__ 
         d = __fdiv_rn(1.f, iscale);
     }
     *(uint32_t *)(blkp + Q8K_QS + 4 * lane) = packed;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += dpp_i<0xB1>(s);  // quad_perm [1,0,3,2]
+    s += dpp_i<0x4E>(s);  // quad_perm [2,3,0,1]
     if ((lane & 3) == 0) *(int16_t *)(blkp + Q8K_BSUMS + 2 * (lane >> 2)) = (int16_t)s;
     if (lane == 0) *(float *)blkp = d;
 }
@@ -77,12 +78,16 @@ hipError_t launch_quantize_q8_K(const void *x, int64_t k, int64_t ne1, int64_t n
     if (nblocks == 0) return hipSuccess;
     const bool vec = ((uintptr_t)x % 16 == 0) && s1 % 16 == 0 && s2 % 16 == 0 && s3 % 16 == 0;
     const dim3 grid((unsigned)((nblocks + 3) / 4));
-    if (vec)
-        k_quantize_q8_K<true><<<grid, 256, 0, stream>>>((const char *)x, nbk, nblocks, ne1, ne2, s1, s2, s3,
-                                                        (uint8_t *)y);
-    else
-        k_quantize_q8_K<false><<<grid, 256, 0, stream>>>((const char *)x, nbk, nblocks, ne1, ne2, s1, s2, s3,
-                                                         (uint8_t *)y);
+    const char *xc = (const char *)x;
+    uint8_t *yc = (uint8_t *)y;
+    if (nblocks + 4 < (int64_t)INT32_MAX) {
+        const int32_t b = (int32_t)nbk, n = (int32_t)nblocks, e1 = (int32_t)ne1, e2 = (int32_t)ne2;
+        if (vec) k_quantize_q8_K<true, int32_t><<<grid, 256, 0, stream>>>(xc, b, n, e1, e2, s1, s2, s3, yc);
+        else k_quantize_q8_K<false, int32_t><<<grid, 256, 0, stream>>>(xc, b, n, e1, e2, s1, s2, s3, yc);
+    } else {
+        if (vec) k_quantize_q8_K<true, int64_t><<<grid, 256, 0, stream>>>(xc, nbk, nblocks, ne1, ne2, s1, s2, s3, yc);
+        else k_quantize_q8_K<false, int64_t><<<grid, 256, 0, stream>>>(xc, nbk, nblocks, ne1, ne2, s1, s2, s3, yc);
+    }
     return hipGetLastError();
 }
 
