@@ -36,12 +36,7 @@ __device__ __forceinline__ int load_id(const uint8_t *ids, int64_t s0, int64_t s
 // Exclusive scan of v over the 256 threads of the block; returns the prefix, *total gets the sum.
 __device__ int block_exclusive_scan(int v, int *lds_tmp, int *total) {
     const int lane = lane_id(), wid = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
+    const int x = wave_incl_scan(v);
     if (lane == 63) lds_tmp[wid] = x;
     __syncthreads();
     int base = 0, sum = 0;

@@ -60,20 +60,6 @@ __device__ __forceinline__ int moe_id(const MoeArgs &m, int s) {
     return e >= 0 && e < m.n_expert ? e : -1;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave: DPP row shifts within each row of 16 lanes, then
-// the row totals (read lane by lane) added to the rows after them. No LDS round trips (a __shfl_up scan
-// is six of them).
-__device__ __forceinline__ int wave_incl_scan(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-    const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31);
-    const int t2 = __builtin_amdgcn_readlane(v, 47);
-    const int row = (threadIdx.x & 63) >> 4;
-    return v + (row == 0 ? 0 : row == 1 ? t0 : row == 2 ? t0 + t1 : t0 + t1 + t2);
-}
-
 // Routing in LDS, identical in every workgroup: routed experts in increasing expert order, each with its
 // slots (in arbitrary order: every slot is an independent output column).
 __device__ void moe_route(const MoeArgs &m, MoeRoute &r) {
