@@ -20,9 +20,10 @@
 namespace tq {
 
 constexpr int ROUTER_THREADS = 256;
-constexpr int ROUTER_SLICE = 8;  // experts per logits workgroup
+constexpr int ROUTER_WAVES = 4;  // waves per logits workgroup; a slice is ROUTER_WAVES * EPW experts
 constexpr int ROUTER_FUSED_MAX_TOK = 4096;  // tokens of a one-launch router call
 constexpr int ROUTER_CHUNK = 2048;          // row elements whose loads are all issued up front
+constexpr int ROUTER_EPW1_MAX_TOK = 2;      // tokens up to which a wave takes one expert (measured: 4 and 8 are faster with two)
 
 // Whole-wave reductions by DPP row shifts (inclusive within each row of 16 lanes) and the four row
 // totals read lane by lane: no LDS round trips (a __shfl_xor tree is six dependent ds_bpermutes).
@@ -73,9 +74,9 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // live in device memory, zero when the module loads, and each last arriver resets its token's).
 __device__ unsigned g_router_arrive[ROUTER_FUSED_MAX_TOK];
 
-template <int PER, bool FUSED>
+template <int PER, bool FUSED, int EPW>
 __global__ __launch_bounds__(ROUTER_THREADS) void k_router_logits(RouterArgs a) {
-    static_assert(ROUTER_SLICE == 2 * (ROUTER_THREADS / 64), "two experts per wave");
+    static_assert(ROUTER_WAVES == ROUTER_THREADS / 64 && (EPW == 1 || EPW == 2), "one or two experts per wave");
     extern __shared__ __align__(16) float xs[];  // the token's xn, n_embd floats
     __shared__ double part[ROUTER_THREADS / 64];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -84,13 +85,16 @@ __global__ __launch_bounds__(ROUTER_THREADS) void k_router_logits(RouterArgs a) 
     // masked use): the wave's two gate rows, the token's row and the norm weights arrive together, while
     // the row is normalized (a load behind a branch or a barrier would wait for what comes before it).
     constexpr int XCH = ROUTER_CHUNK / ROUTER_THREADS, GCH = ROUTER_CHUNK / 64;
-    const int last = a.n_embd - 1, e0 = blockIdx.x * ROUTER_SLICE;
+    const int last = a.n_embd - 1, e0 = blockIdx.x * ROUTER_WAVES * EPW;
     const int ea = e0 + wave, eb = e0 + wave + ROUTER_THREADS / 64;
     const float *wa = a.gate + (int64_t)min(ea, a.n_expert - 1) * a.g_s1;
     const float *wb = a.gate + (int64_t)min(eb, a.n_expert - 1) * a.g_s1;
     float ga[GCH], gb[GCH], xv[XCH], nv[XCH];
 #pragma unroll
-    for (int u = 0; u < GCH; ++u) ga[u] = wa[min(64 * u + lane, last)], gb[u] = wb[min(64 * u + lane, last)];
+    for (int u = 0; u < GCH; ++u) {
+        ga[u] = wa[min(64 * u + lane, last)];
+        gb[u] = EPW == 2 ? wb[min(64 * u + lane, last)] : 0.f;
+    }
 #pragma unroll
     for (int u = 0; u < XCH; ++u) {
         const int i = min(u * ROUTER_THREADS + tid, last);
@@ -135,17 +139,17 @@ __global__ __launch_bounds__(ROUTER_THREADS) void k_router_logits(RouterArgs a) 
         const int i = 64 * u + lane;
         const float xi = i < a.n_embd ? xs[min(i, last)] : 0.f;
         pa[u & 3] = fmaf(ga[u], xi, pa[u & 3]);
-        pb[u & 3] = fmaf(gb[u], xi, pb[u & 3]);
+        if (EPW == 2) pb[u & 3] = fmaf(gb[u], xi, pb[u & 3]);
     }
     for (int i = ROUTER_CHUNK + lane; i < a.n_embd; i += 64) {
         pa[0] = fmaf(wa[i], xs[i], pa[0]);
-        pb[0] = fmaf(wb[i], xs[i], pb[0]);
+        if (EPW == 2) pb[0] = fmaf(wb[i], xs[i], pb[0]);
     }
     const float acc_a = wave_sum_f32((pa[0] + pa[1]) + (pa[2] + pa[3]));
-    const float acc_b = wave_sum_f32((pb[0] + pb[1]) + (pb[2] + pb[3]));
+    const float acc_b = EPW == 2 ? wave_sum_f32((pb[0] + pb[1]) + (pb[2] + pb[3])) : 0.f;
     if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < EPW; ++r) {
             const int e = r ? eb : ea;
             const float acc = r ? acc_b : acc_a;
             if (e >= a.n_expert) continue;
@@ -232,19 +236,27 @@ __global__ __launch_bounds__(64) void k_router_topk(RouterArgs a) {
     router_topk<PER>(a, t, [&](int e) { return l[e]; });
 }
 
-template <int PER>
-static hipError_t launch_router_per(const RouterArgs &a, hipStream_t stream) {
-    const dim3 g1((unsigned)((a.n_expert + ROUTER_SLICE - 1) / ROUTER_SLICE), (unsigned)a.ntok);
+template <int PER, int EPW>
+static hipError_t launch_router_epw(const RouterArgs &a, hipStream_t stream) {
+    constexpr int SLICE = ROUTER_WAVES * EPW;
+    const dim3 g1((unsigned)((a.n_expert + SLICE - 1) / SLICE), (unsigned)a.ntok);
     const size_t lds = (size_t)a.n_embd * sizeof(float);
     if (a.ntok <= ROUTER_FUSED_MAX_TOK) {
-        k_router_logits<PER, true><<<g1, ROUTER_THREADS, lds, stream>>>(a);
+        k_router_logits<PER, true, EPW><<<g1, ROUTER_THREADS, lds, stream>>>(a);
         return hipGetLastError();
     }
-    k_router_logits<PER, false><<<g1, ROUTER_THREADS, lds, stream>>>(a);
+    k_router_logits<PER, false, EPW><<<g1, ROUTER_THREADS, lds, stream>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_router_topk<PER><<<dim3((unsigned)a.ntok), 64, 0, stream>>>(a);
     return hipGetLastError();
+}
+
+// Few tokens: one expert per wave, twice the workgroups, half the gate rows each (the launch is
+// latency-bound); more tokens: two per wave, the token's row normalized half as often.
+template <int PER>
+static hipError_t launch_router_per(const RouterArgs &a, hipStream_t stream) {
+    return a.ntok <= ROUTER_EPW1_MAX_TOK ? launch_router_epw<PER, 1>(a, stream) : launch_router_epw<PER, 2>(a, stream);
 }
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t stream) {
