@@ -143,6 +143,13 @@ def test_sum_experts_matches_oracle(gpu):
     view = wide[:, ::2, :]
     got = ggml.sum_experts(view).cpu().numpy()
     np.testing.assert_array_equal(got, O.sum_experts(view.cpu().numpy()))
+    # slot counts around the kernel's batch of 8 loads, and all -0.0 rows (a stand-in +0 would show)
+    for n_used in (1, 7, 9, 11, 16):
+        e2 = rng.standard_normal((2, n_used, 96)).astype(np.float32)
+        e2[:, :, :5] = -0.0
+        got = ggml.sum_experts(torch.from_numpy(e2).to(gpu)).cpu().numpy()
+        np.testing.assert_array_equal(got, O.sum_experts(e2))
+        assert np.all(np.signbit(got[:, :5])), f"n_used={n_used}: -0.0 sums lost their sign"
 
 
 @pytest.mark.parametrize("tokens", [1, 2, 4, 16, 32, 40])

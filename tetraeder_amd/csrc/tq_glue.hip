@@ -35,11 +35,21 @@ __global__ __launch_bounds__(256) void k_scale_rows(float *__restrict__ x, int64
 __global__ __launch_bounds__(256) void k_sum_experts(const float *__restrict__ x, int64_t n_embd, int n_used,
                                                      int64_t x_s1, int64_t x_s2, float *__restrict__ out,
                                                      int64_t o_s1) {
+    constexpr int B = 8;  // slot loads in flight per batch (a loop over n_used would wait for each)
     const int64_t t = blockIdx.y;
     const float *xt = x + t * x_s2;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_embd; e += (int64_t)gridDim.x * blockDim.x) {
-        float acc = xt[e];
-        for (int j = 1; j < n_used; ++j) acc += xt[j * x_s1 + e];
+        float acc = 0.f;
+        for (int j0 = 0; j0 < n_used; j0 += B) {
+            float v[B];
+#pragma unroll
+            for (int i = 0; i < B; ++i) v[i] = xt[(int64_t)min(j0 + i, n_used - 1) * x_s1 + e];
+            // left to right, only the slots that exist (adding a stand-in 0 would turn -0 into +0)
+            acc = j0 == 0 ? v[0] : acc + v[0];
+#pragma unroll
+            for (int i = 1; i < B; ++i)
+                if (j0 + i < n_used) acc += v[i];
+        }
         out[t * o_s1 + e] = acc;
     }
 }
