@@ -49,6 +49,8 @@ __device__ int block_exclusive_scan(int v, int *lds_tmp, int *total) {
     return base + x - v;
 }
 
+constexpr int ROUTE_IDS = 8;  // ids per thread in flight while routing
+
 __global__ __launch_bounds__(ROUTE_THREADS) void k_mmid_route(MmidArgs a) {
     const int n_slots = a.n_used * a.ntok, E = a.n_expert;
     if (blockIdx.x > 0) {
@@ -66,9 +68,22 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_mmid_route(MmidArgs a) {
     int *cnt = lds_i, *pos = lds_i + E, *tmp = lds_i + 2 * E;
     for (int e = threadIdx.x; e < E; e += ROUTE_THREADS) cnt[e] = 0;
     __syncthreads();
-    for (int s = threadIdx.x; s < n_slots; s += ROUTE_THREADS) {
-        const int e = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, s);
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    // ids are read ROUTE_IDS per thread at a time, all in flight together (clamped index, masked use):
+    // a loop of one load and one atomic per slot would wait for every load
+    auto ids_batch = [&](int s0, int (&ev)[ROUTE_IDS]) {
+#pragma unroll
+        for (int i = 0; i < ROUTE_IDS; ++i)
+            ev[i] = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, min(s0 + i * ROUTE_THREADS, n_slots - 1));
+#pragma unroll
+        for (int i = 0; i < ROUTE_IDS; ++i)
+            if (s0 + i * ROUTE_THREADS >= n_slots || ev[i] < 0 || ev[i] >= E) ev[i] = -1;
+    };
+    for (int s0 = threadIdx.x; s0 < n_slots; s0 += ROUTE_IDS * ROUTE_THREADS) {
+        int ev[ROUTE_IDS];
+        ids_batch(s0, ev);
+#pragma unroll
+        for (int i = 0; i < ROUTE_IDS; ++i)
+            if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
     }
     __syncthreads();
     // each thread scans a contiguous chunk of experts
@@ -90,9 +105,12 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_mmid_route(MmidArgs a) {
     }
     if (threadIdx.x == 0) a.route[0] = n_active, a.route[1] = n_valid;
     __syncthreads();
-    for (int s = threadIdx.x; s < n_slots; s += ROUTE_THREADS) {
-        const int e = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, s);
-        if (e >= 0 && e < E) slot[atomicAdd(&pos[e], 1)] = s;
+    for (int s0 = threadIdx.x; s0 < n_slots; s0 += ROUTE_IDS * ROUTE_THREADS) {
+        int ev[ROUTE_IDS];
+        ids_batch(s0, ev);
+#pragma unroll
+        for (int i = 0; i < ROUTE_IDS; ++i)
+            if (ev[i] >= 0) slot[atomicAdd(&pos[ev[i]], 1)] = s0 + i * ROUTE_THREADS;
     }
 }
 
