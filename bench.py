@@ -7,8 +7,8 @@ roofline: the GEMV kernel alone (activation already Q8_K), timed with HIP events
 launched on, algorithmic bytes = weight bytes per launch.
 cpu_baseline: the restated iqk AVX-512 VNNI CPU path (oracle/tq_cpu_baseline.c) on the host cores,
 same weight bytes, Q8_K quantization included, median of calls within a bounded budget.
-secondary: the other workloads (Q4_K GEMV 4096 x 4096 batch 1, attention projections, MoE step and
-router, prefill, expert slot uploads from host memory).
+secondary: the other workloads (Q4_K GEMV 4096 x 4096 batch 1, attention projections, MUL_MAT_ID at
+prefill sizes, MoE step and router, prefill, expert slot uploads from host memory).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -430,6 +430,23 @@ def bench_secondary(ggml, torch, dev):
             res[f"attn_{name}_proj_{k}x{n}_m{m}"] = {"op_us": round(us, 2), "GBps": round(wb / us / 1e3, 1)}
         del W
         log(f"attn {name}: " + ", ".join(f"m{m} {res[f'attn_{name}_proj_{k}x{n}_m{m}']['op_us']}us" for m in (1, 4, 16, 32)))
+    torch.cuda.empty_cache()
+    # MUL_MAT_ID at prefill sizes: gate Q4_K [2048 -> 768] x 128 experts, top-8 of 512 and 2048 tokens
+    E, k, n = 128, 2048, 768
+    w = make_weights(ggml, torch, ty, k, n * E, 1, seed=3, dev=dev)[0]
+    w = ggml.QTensor(w.type, (k, n, E), w.data)
+    import numpy as np
+    for T in (512, 2048):
+        ids = torch.from_numpy(moe_ids(np, T, seed=T)).to(dev)
+        x = torch.randn((T, 1, k), device=dev)
+        out = torch.empty((T, 8, n), device=dev)
+        ws = torch.empty(max(1, ggml.mul_mat_id_workspace_size(w, x, ids)), dtype=torch.uint8, device=dev)
+        us = time_graph(torch, lambda i: ggml.mul_mat_id(w, x, ids, out=out, workspace=ws), 4)
+        valid = int((ids >= 0).sum().item())
+        res[f"mul_mat_id_q4_K_2048x768x128_T{T}"] = {"op_us": round(us, 1),
+                                                     "int_TOPS": round(2 * valid * n * k / us / 1e6, 1)}
+        log(f"mul_mat_id T={T}: {res[f'mul_mat_id_q4_K_2048x768x128_T{T}']}")
+    del w
     torch.cuda.empty_cache()
     return res
 
