@@ -107,9 +107,22 @@ template <class Fn> __device__ __forceinline__ void moe_column_passes(int cnt, F
 
 __device__ __forceinline__ float moe_silu(float x) { return x / (1.0f + expf(-x)); }
 
-// Work weight of an expert with cnt columns, in proportion to the GEMV core's instructions per item:
-// the column passes of up to MOE_NC columns cost 5 + 2 per extra column (on MI355X a 3-token expert,
-// then padded to 4 columns, streamed its rows 2.2 times slower than a 1-token expert).
+// Work weights of an expert with cnt columns, summed over its column passes of up to MOE_NC columns.
+// moe_cost_measured: the measured time of a pass (both phases, per workgroup times workgroups,
+// Qwen3-30B-A3B shapes on MI355X): 1, 1.08, 1.25 and 1.6 times a 1-column pass, in tenths; it deals
+// the proportional deal best where an expert gets 3 to 11 workgroups (8 tokens: 43.2 -> 41.4 us).
+// moe_cost: 5 + 2 per extra column, which the min-max deal (16 tokens: 60.8 against 61.5 us with the
+// measured weights) and the proportional deal with 12 or more workgroups per expert (2 tokens: 20.2
+// against 20.8 us) do better with.
+__device__ __forceinline__ int moe_cost_measured(int cnt) {
+    int c = 0;
+    for (int c0 = 0; c0 < cnt; c0 += MOE_NC) {
+        const int n = min(MOE_NC, cnt - c0);
+        c += n == 1 ? 10 : n == 2 ? 11 : n == 3 ? 13 : 16;
+    }
+    return c;
+}
+
 __device__ __forceinline__ int moe_cost(int cnt) {
     int c = 0;
     for (int c0 = 0; c0 < cnt; c0 += MOE_NC) {
@@ -204,14 +217,18 @@ __device__ int moe_deal(const MoeRoute &r, int *first, int *cls, int *mine) {
             // one each, the spare in proportion to the cost prefix: first[a] = a + spare * pre(a) / total
             const int per = (n_act + 63) / 64, a0 = min(n_act, lane * per), a1 = min(n_act, a0 + per);
             int c = 0;
-            for (int a = a0; a < a1; ++a) c += moe_cost(r.start[a + 1] - r.start[a]);
+            // the measured weights where an expert gets fewer than 12 workgroups; with more, each
+            // workgroup's share is short and latency-bound and the extra columns weigh more
+            const bool meas = 12 * n_act > nwg;
+            auto cost = [&](int cnt) { return meas ? moe_cost_measured(cnt) : moe_cost(cnt); };
+            for (int a = a0; a < a1; ++a) c += cost(r.start[a + 1] - r.start[a]);
             const int pc = wave_incl_scan(c);
             const int total = __builtin_amdgcn_readlane(pc, 63);
             const int64_t spare = nwg - n_act;
             int pre = pc - c;
             for (int a = a0; a < a1; ++a) {
                 first[a] = a + (int)(spare * pre / total);
-                pre += moe_cost(r.start[a + 1] - r.start[a]);
+                pre += cost(r.start[a + 1] - r.start[a]);
             }
             if (lane == 63) first[n_act] = nwg;
         }
