@@ -59,6 +59,43 @@ def test_gemv_one_column(gpu, tname, k, n):
     check(y[0], want[0], f"{tname} k={k} n={n}", bound, ref)
 
 
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_q4_K_4096x4096_full_size(gpu, m):
+    """The single Q4_K MUL_MAT of the reference's CPU benchmark at its own shape: weight 4096 x 4096
+    (N(0, 0.02), 9,437,184 bytes), activation batch 1 (also 2 and 4) N(0, 1), every output row against
+    the oracle and the per-row f64 bound. On a 256-CU part the batch-1 stream runs two passes per wave,
+    so the second LDS slot and the stash flush after a multi-pass window are exercised."""
+    _case(f"q4_K 4096x4096 m={m}")
+    ty = ggml.Type.Q4_K
+    k = n = 4096
+    w = make_weights(ty, k, n, 1, seed=4096 + m, device=gpu)
+    x = normal((m, k), 40960 + m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    raw = w.data.cpu().numpy()
+    want = O.mul_mat(ty.id, raw, k, n, x)[0]
+    for c in range(m):
+        ref, bound = O.ref_f64(ty.id, raw, k, x[c])
+        check(y[c], want[c], f"q4_K 4096x4096 m={m} col {c}", bound, ref)
+
+
+@pytest.mark.parametrize("k,n", [(4096, 8192), (4096, 12289), (4096, 40000), (1024, 300000), (1024, 600000)])
+@pytest.mark.parametrize("m", [1, 2])
+def test_q4_K_multi_pass(gpu, k, n, m):
+    """Q4_K with several LDS-stream passes per wave (2048 waves on 256 CUs): at K = 4096 (one row per
+    pass) 8192 rows (4 passes per wave), a ragged 12289 (one wave's last pass holds the last row) and
+    40000 (about 20 passes); at K = 1024 (four rows per pass) 300000 and 600000 rows, 37 and 73 passes
+    per wave, past the 32 (two columns) and 64 (one column) passes whose row totals one stash window
+    holds, so stashed totals are flushed between windows. Every row is checked."""
+    _case(f"q4_K k={k} n={n} m={m}")
+    ty = ggml.Type.Q4_K
+    w = make_weights(ty, k, n, 1, seed=n + 7 * m, device=gpu)
+    x = normal((m, k), n + m)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q4_K k={k} n={n} m={m}")
+    assert np.all(np.isfinite(y))
+
+
 @pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
 @pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 9, 16, 17, 32])
 def test_gemv_columns(gpu, tname, m):

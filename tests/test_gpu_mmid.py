@@ -150,15 +150,28 @@ def test_mmid_golden(gpu, tname):
     check(got, g["y"], g["ids"], f"golden {tname}")
 
 
-def test_workspace_argument(gpu):
+def test_mul_mat_id_workspace_argument(gpu):
+    """Decode-size MUL_MAT_ID (up to 256 slots) routes in LDS and quantizes inside its workgroups: it
+    reports no workspace and runs with none (nothing is allocated, so it is capture-safe). Above 256
+    slots the reported size is needed and a smaller workspace is rejected."""
     _case("workspace")
-    w = make_experts(ggml.Type.Q4_K, 512, 16, 8, seed=4, device=gpu)
-    ids = torch.from_numpy(make_ids(8, 2, 5, 20, np.random.default_rng(1))).to(gpu)
-    b = torch.from_numpy(normal((5, 1, 512), 4)).to(gpu)
-    need = ggml.mul_mat_id_workspace_size(w, b, ids)
+    ty = ggml.Type.Q4_K
+    k, n, E, used = 512, 64, 16, 4
+    w = make_experts(ty, k, n, E, seed=11, device=gpu)
+    rng = np.random.default_rng(12)
+    ids_small = torch.from_numpy(make_ids(E, used, 8, 20, rng)).to(gpu)
+    b_small = torch.from_numpy(normal((8, 1, k), 13)).to(gpu)
+    assert ggml.mul_mat_id_workspace_size(w, b_small, ids_small) == 0
+    a = ggml.mul_mat_id(w, b_small, ids_small, workspace=torch.empty(0, dtype=torch.uint8, device=gpu))
+    want = O.mul_mat_id(ty.id, w.data.cpu().numpy(), k, n, E, b_small.cpu().numpy(), ids_small.cpu().numpy())
+    check(a.cpu().numpy(), want, ids_small.cpu().numpy(), "decode size, no workspace")
+    ids_big = torch.from_numpy(make_ids(E, used, 80, 20, rng)).to(gpu)
+    b_big = torch.from_numpy(normal((80, 1, k), 14)).to(gpu)
+    need = ggml.mul_mat_id_workspace_size(w, b_big, ids_big)
+    assert need > 0
     ws = torch.empty(need, dtype=torch.uint8, device=gpu)
-    a1 = ggml.mul_mat_id(w, b, ids, workspace=ws)
-    a2 = ggml.mul_mat_id(w, b, ids)
-    assert torch.equal(a1, a2)
+    c = ggml.mul_mat_id(w, b_big, ids_big, workspace=ws)
+    d = ggml.mul_mat_id(w, b_big, ids_big)
+    assert torch.equal(c, d)
     with pytest.raises(ggml.Compute):
-        ggml.mul_mat_id(w, b, ids, workspace=ws[: need - 1])
+        ggml.mul_mat_id(w, b_big, ids_big, workspace=ws[: need // 2])

@@ -127,3 +127,15 @@ def test_router_feeds_the_moe_step_in_a_graph(gpu, T):
         torch.cuda.synchronize()
         assert torch.equal(out, want)
     assert ggml.moe_sync_errors(clear=True) == 0
+
+
+def test_router_softmax_closed_form(gpu):
+    """logits {0, ln 3, ln 4} (x = [1, 1], eps 0, one-hot gate rows) give probabilities {1/8, 3/8, 4/8}:
+    top-2 is [2, 1] with weights {4/7, 3/7}."""
+    _case("closed form")
+    x = torch.ones((1, 2), device=gpu)
+    gate = torch.tensor([[0.0, 0.0], [float(np.log(3.0)), 0.0], [0.0, float(np.log(4.0))]], device=gpu)
+    xn, w, ids = ggml.moe_router(x, torch.ones(2, device=gpu), gate, 0.0, 2)
+    assert torch.equal(xn, x)
+    assert ids.cpu().tolist() == [[2, 1]]
+    np.testing.assert_allclose(w.cpu().numpy()[0, :, 0], [4 / 7, 3 / 7], rtol=0, atol=2e-7)

@@ -151,3 +151,22 @@ def test_router_top_k_order_and_weights():
     np.testing.assert_allclose(xn, -0.5, rtol=1e-6)
     _, _, _, ids = O.router(np.ones((1, 4), np.float32), np.ones(4, np.float32), np.ones((3, 4), np.float32), 1e-6, 2)
     assert ids.tolist() == [[0, 1]]
+
+
+def test_router_softmax_closed_form():
+    """soft_max in closed form: logits {0, ln 3} give probabilities {1/4, 3/4} (e^0 : e^ln3 = 1 : 3), and
+    {0, ln 3, ln 4} give {1/8, 3/8, 4/8}. x = [1, 1] with eps 0 normalizes to itself exactly, and one-hot
+    gate rows make the logits the chosen values. Top-2 of the second case is [2, 1] with weights
+    {4/7, 3/7} (the selected probabilities over their sum)."""
+    x = np.ones((1, 2), np.float32)
+    gate = np.array([[0.0, 0.0], [np.log(3.0), 0.0]], dtype=np.float32)
+    xn, probs, w, ids = O.router(x, np.ones(2, np.float32), gate, 0.0, 2)
+    np.testing.assert_array_equal(xn, x)
+    np.testing.assert_allclose(probs[0], [0.25, 0.75], rtol=0, atol=2e-7)
+    assert ids.tolist() == [[1, 0]]
+    np.testing.assert_allclose(w[0], [0.75, 0.25], rtol=0, atol=2e-7)
+    gate3 = np.array([[0.0, 0.0], [np.log(3.0), 0.0], [0.0, np.log(4.0)]], dtype=np.float32)
+    _, probs, w, ids = O.router(x, np.ones(2, np.float32), gate3, 0.0, 2)
+    np.testing.assert_allclose(probs[0], [0.125, 0.375, 0.5], rtol=0, atol=2e-7)
+    assert ids.tolist() == [[2, 1]]
+    np.testing.assert_allclose(w[0], [4 / 7, 3 / 7], rtol=0, atol=2e-7)

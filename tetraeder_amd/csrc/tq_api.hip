@@ -383,7 +383,10 @@ static int check_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_te
     return TQ_STATUS_SUCCESS;
 }
 
+// Decode-size MUL_MAT_ID (k_mmid_small) routes in LDS and quantizes its activations inside the workgroups:
+// it needs no workspace. Larger calls hold the Q8_K copy of b and the routing lists.
 static size_t mmid_workspace(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids) {
+    if (ids->ne[0] * ids->ne[1] <= mmid_small_max_slots()) return 0;
     return q8_bytes(b) + align_up(mmid_route_bytes((int)as->ne[2], ids->ne[0] * ids->ne[1]), 256);
 }
 
@@ -401,8 +404,11 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     const size_t need = mmid_workspace(as, b, ids);
     if (workspace && workspace_size < need)
         return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
-    if (!ws) return rc;
+    uint8_t *ws = nullptr;
+    if (need) {
+        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+        if (!ws) return rc;
+    }
     hipStream_t s = (hipStream_t)stream;
     MmidArgs m{};
     m.w = (const uint8_t *)as->data;
@@ -421,7 +427,7 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     m.dst = (float *)dst->data;
     m.d_s1 = (int64_t)(dst->nb[1] / 4);
     m.d_s2 = (int64_t)(dst->nb[2] / 4);
-    m.route = (int32_t *)(ws + q8_bytes(b));
+    m.route = ws ? (int32_t *)(ws + q8_bytes(b)) : nullptr;
     if (n_used * T <= mmid_small_max_slots()) {
         // decode: one launch, routing resolved per workgroup, activations quantized in LDS
         const int b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0;

@@ -152,4 +152,10 @@ __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b)
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
+// A workgroup barrier that orders LDS accesses only: the wave's own LDS reads and writes are complete
+// (lgkmcnt 0) before it waits for the others, while its vector memory loads stay in flight (LDS DMA
+// fills of wave-private buffers among them: __syncthreads' release fence would wait for every one).
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace tq

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv(GemvArgs a) {
             const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
             stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
         }
-        __syncthreads();
+        lds_barrier();  // the weight loads issued before the staging stay in flight
     };
 
     const int ncols = a.ncols;
@@ -54,6 +54,9 @@ template <int F, int NC, int LPR> constexpr int gemv_dma_act_bytes() {
 // faster here: on the Q6_K 151936 x 2048 head two slots take 39.9 us, three 41.1 us, four 41.7 us (the
 // plain read of as many bytes is fastest at 2-3 KB in flight per wave too).
 constexpr int GEMV_DMA_NS = 2;
+// Activation blocks per wave whose floats are loaded ahead of the weight fills (F32 activations are
+// quantized in the workgroup up to 16 column blocks: two per wave).
+constexpr int GEMV_DMA_PRE = 2;
 
 // The same over contiguous rows through wave-private LDS slots (gemv_rows_dma).
 template <int F, int NC, int LPR>
@@ -63,28 +66,58 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv_dma(GemvArgs a) {
     __shared__ float stash[GEMV_WAVES][GEMV_DMA_STASH];
     __shared__ __align__(16) uint8_t lds[gemv_dma_act_bytes<F, NC, LPR>()];
     const int nb = a.nb, wv = threadIdx.x >> 6;
-    const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
-    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
+    // The batch of this workgroup; a single one (decode) skips the index divisions, which would sit on
+    // the path to the first load.
+    int i2 = 0, i3 = 0, j2 = 0, j3 = 0;
+    if (a.nbatch > 1) {
+        i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
+        j2 = i2 / a.r2, j3 = i3 / a.r3;
+    }
+    const uint8_t *w = a.w + (int64_t)j2 * a.w_s2 + (int64_t)j3 * a.w_s3;
     const uint8_t *q8 = a.q8 + ((int64_t)(i3 * a.ne12 + i2) * a.q8_cols + a.col0) * nb * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3 + a.col0 * a.d_s1;
 
     uint8_t *lds_qs = lds;
     int16_t *lds_bs = (int16_t *)(lds + NC * nb * ACT_QS_PITCH);
     float *lds_d = (float *)(lds + NC * nb * (ACT_QS_PITCH + ACT_BS_BYTES));
+    // F32 activations: wave wv quantizes column blocks wv, wv + 8, ... (block i is column i / nb, super-block
+    // i % nb). The floats of its first GEMV_DMA_PRE blocks are loaded before the weight fills are issued,
+    // so they return first and the quantization overlaps the weights' flight (loads return in order).
+    // (The address of b is formed without a branch, and as a global pointer: integer address arithmetic
+    // makes the compiler issue flat loads, which a wait for the kernel arguments then waits for.)
+    const int ncols = a.ncols, nblk = a.b ? ncols * nb : 0;
+    const float *b0 = a.b + (a.b ? i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1 : 0);
+    const int64_t b_s1 = a.b_s1;
+    const bool b_vec = a.b_vec != 0;
+    auto block_src = [&](int i) {
+        const int c = NC == 1 ? 0 : i / nb;
+        return b0 + c * b_s1 + (size_t)(i - c * nb) * QK;
+    };
+    float pv[GEMV_DMA_PRE][4];
+    auto pre = [&]() {
+#pragma unroll
+        for (int r = 0; r < GEMV_DMA_PRE; ++r) {
+            const int i = wv + r * GEMV_WAVES;
+            if (i < nblk) load_block_f32(block_src(i), b_vec, pv[r]);
+        }
+    };
     auto stage = [&]() {
         if (a.b) {
-            const float *b = a.b + i2 * a.b_s2 + i3 * a.b_s3 + a.col0 * a.b_s1;
-            const int64_t b_s1 = a.b_s1;
-            stage_activations_f32<F, NC>([&](int c) { return b + c * b_s1; }, a.b_vec != 0, nb, a.ncols, lds_qs,
-                                         lds_bs, lds_d);
+#pragma unroll
+            for (int r = 0; r < GEMV_DMA_PRE; ++r) {
+                const int i = wv + r * GEMV_WAVES;
+                if (i < nblk) wave_quantize_vals_to_lds<F>(pv[r], i, lds_qs, lds_bs, lds_d);
+            }
+            for (int i = wv + GEMV_DMA_PRE * GEMV_WAVES; i < nblk; i += GEMV_WAVES)
+                wave_quantize_to_lds<F>(block_src(i), b_vec, i, lds_qs, lds_bs, lds_d);
+            zero_columns<NC>(ncols, nb, lds_qs, lds_bs, lds_d);
         } else {
             const int64_t col_bytes = (int64_t)nb * Q8K_BYTES;
-            stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, a.ncols, lds_qs, lds_bs, lds_d);
+            stage_activations<F, NC>([&](int c) { return q8 + c * col_bytes; }, nb, ncols, lds_qs, lds_bs, lds_d);
         }
-        __syncthreads();
+        lds_barrier();  // the weight fills stay in flight
     };
 
-    const int ncols = a.ncols;
     const int64_t d_s1 = a.d_s1;
     auto store = [&](int c, int row, float v) {
         if (c < ncols) dst[c * d_s1 + row] = v;
@@ -92,7 +125,7 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv_dma(GemvArgs a) {
     const int wave = blockIdx.x * GEMV_WAVES + wv, nwaves = gridDim.x * GEMV_WAVES;
     uint8_t *const slots[GEMV_DMA_NS] = {slot0[wv], slot1[wv]};
     gemv_rows_dma<F, NC, LPR, GEMV_DMA_NS>(w, (int)a.nrows, nb, wave, nwaves, slots, stash[wv], lds_qs, lds_bs, lds_d,
-                                           stage, store);
+                                           pre, stage, store);
 }
 
 // The LDS stream takes contiguous rows whose row bytes are a multiple of 16 (every wave load of 16-byte

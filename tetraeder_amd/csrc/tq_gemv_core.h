@@ -132,12 +132,9 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
     if (lane == 0) lds_d[cb] = d;
 }
 
-// The same for 256 floats read from src (lane l takes src[4l .. 4l+3]).
-template <int F>
-__device__ __forceinline__ void wave_quantize_to_lds(const float *__restrict__ src, bool vec, int cb, uint8_t *lds_qs,
-                                                     int16_t *lds_bs, float *lds_d) {
+// Lane l's four floats src[4l .. 4l+3] of a 256-float block (one 16-byte load when vec).
+__device__ __forceinline__ void load_block_f32(const float *__restrict__ src, bool vec, float (&v)[4]) {
     const int lane = lane_id();
-    float v[4];
     if (vec) {
         const float4 f = *(const float4 *)(src + 4 * lane);
         v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
@@ -145,6 +142,14 @@ __device__ __forceinline__ void wave_quantize_to_lds(const float *__restrict__ s
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[4 * lane + j];
     }
+}
+
+// The same for 256 floats read from src (lane l takes src[4l .. 4l+3]).
+template <int F>
+__device__ __forceinline__ void wave_quantize_to_lds(const float *__restrict__ src, bool vec, int cb, uint8_t *lds_qs,
+                                                     int16_t *lds_bs, float *lds_d) {
+    float v[4];
+    load_block_f32(src, vec, v);
     wave_quantize_vals_to_lds<F>(v, cb, lds_qs, lds_bs, lds_d);
 }
 
@@ -216,9 +221,34 @@ template <> struct Item<FMT_Q6K> {
     }
 };
 
-template <int NC>
-__device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
-                                             const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+// One lane's activation operands of one column and super-block: its 64 Q8_K bytes, its bsums slots (Q4_K
+// the first dword: two 32-element sums; Q6_K both: four 16-element sums) and the block's d.
+struct ActOps {
+    uint4 y0, y1, y2, y3;
+    uint2 bs;
+    float d;
+};
+
+// The operands of column block cb for lane u from the LDS staging layout.
+template <int F>
+__device__ __forceinline__ ActOps act_ops(const uint8_t *lds_qs, const int16_t *lds_bs, const float *lds_d, int cb, int u) {
+    ActOps o;
+    const uint8_t *y = lds_qs + cb * ACT_QS_PITCH + u * 64;
+    o.y0 = *(const uint4 *)(y), o.y1 = *(const uint4 *)(y + 16);
+    o.y2 = *(const uint4 *)(y + 32), o.y3 = *(const uint4 *)(y + 48);
+    if (F == FMT_Q4K) {
+        o.bs = uint2{*(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2), 0u};
+    } else {
+        o.bs = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
+    }
+    o.d = lds_d[cb];
+    return o;
+}
+
+// compute_item with the operands of column col from act(col): straight from LDS (compute_item below), or
+// held in registers across passes by a stream whose lanes revisit one super-block.
+template <int NC, class Act>
+__device__ __forceinline__ void compute_item_ops(const Item<FMT_Q4K> &it, int u, Act act, Acc<NC> &acc) {
     const uint4 hdr = it.hdr;
     // an invalid item read a valid stand-in block; zero scales make its contribution exactly 0
     const float d = it.valid ? half_bits_to_float(hdr.x) : 0.f;
@@ -241,10 +271,8 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int
     for (int i = 0; i < 8; ++i) lo[i] = qw[i] & 0x0f0f0f0fu, hi[i] = (qw[i] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
-        const int cb = cb0 + col * nb;
-        const uint8_t *y = lds_qs + cb * ACT_QS_PITCH + u * 64;
-        const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
-        const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
+        const ActOps o = act(col);
+        const uint4 y0 = o.y0, y1 = o.y1, y2 = o.y2, y3 = o.y3;
         int slo = dot4(lo[0], y0.x, 0);
         slo = dot4(lo[1], y0.y, slo), slo = dot4(lo[2], y0.z, slo), slo = dot4(lo[3], y0.w, slo);
         slo = dot4(lo[4], y1.x, slo), slo = dot4(lo[5], y1.y, slo), slo = dot4(lo[6], y1.z, slo);
@@ -253,16 +281,15 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q4K> &it, int u, int
         shi = dot4(hi[1], y2.y, shi), shi = dot4(hi[2], y2.z, shi), shi = dot4(hi[3], y2.w, shi);
         shi = dot4(hi[4], y3.x, shi), shi = dot4(hi[5], y3.y, shi), shi = dot4(hi[6], y3.z, shi);
         shi = dot4(hi[7], y3.w, shi);
-        const uint32_t bsw = *(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2);
+        const uint32_t bsw = o.bs.x;
         const int isum = mad24(sc_lo, slo, mul24(sc_hi, shi));
         const int msum = mad24(m_lo, (int)(int16_t)(bsw & 0xffffu), mul24(m_hi, (int)(int16_t)(bsw >> 16)));
-        acc.v[col] += lds_d[cb] * (d * (float)isum - dmin * (float)msum);
+        acc.v[col] += o.d * (d * (float)isum - dmin * (float)msum);
     }
 }
 
-template <int NC>
-__device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
-                                             const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+template <int NC, class Act>
+__device__ __forceinline__ void compute_item_ops(const Item<FMT_Q6K> &it, int u, Act act, Acc<NC> &acc) {
     const int h = u >> 1, v = u & 1;
     const uint32_t sh = it.sh;
     // Each window's fifth aligned dword is the first dword of another window of the same block, held by a
@@ -307,21 +334,26 @@ __device__ __forceinline__ void compute_item(const Item<FMT_Q6K> &it, int u, int
     }
 #pragma unroll
     for (int col = 0; col < NC; ++col) {
-        const int cb = cb0 + col * nb;
-        const uint8_t *y = lds_qs + cb * ACT_QS_PITCH + u * 64;
-        const uint4 y0 = *(const uint4 *)(y), y1 = *(const uint4 *)(y + 16);
-        const uint4 y2 = *(const uint4 *)(y + 32), y3 = *(const uint4 *)(y + 48);
+        const ActOps o = act(col);
+        const uint4 y0 = o.y0, y1 = o.y1, y2 = o.y2, y3 = o.y3;
         const int S0 = dot4(c0[3], y0.w, dot4(c0[2], y0.z, dot4(c0[1], y0.y, dot4(c0[0], y0.x, 0))));
         const int S1 = dot4(c1[3], y1.w, dot4(c1[2], y1.z, dot4(c1[1], y1.y, dot4(c1[0], y1.x, 0))));
         const int S2 = dot4(c2[3], y2.w, dot4(c2[2], y2.z, dot4(c2[1], y2.y, dot4(c2[0], y2.x, 0))));
         const int S3 = dot4(c3[3], y3.w, dot4(c3[2], y3.z, dot4(c3[1], y3.y, dot4(c3[0], y3.x, 0))));
-        const uint2 bsw = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
+        const uint2 bsw = o.bs;
         const int corr = mad24(sc0, (int)(int16_t)(bsw.x & 0xffffu),
                                mad24(sc1, (int)(int16_t)(bsw.x >> 16),
                                      mad24(sc2, (int)(int16_t)(bsw.y & 0xffffu), mul24(sc3, (int)(int16_t)(bsw.y >> 16)))));
         const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mad24(sc3, S3, mul24(-32, corr)))));
-        acc.v[col] += (lds_d[cb] * d) * (float)isum;
+        acc.v[col] += (o.d * d) * (float)isum;
     }
+}
+
+// The item against the NC columns staged in LDS (column col at column block cb0 + col * nb).
+template <int NC, int F>
+__device__ __forceinline__ void compute_item(const Item<F> &it, int u, int cb0, int nb, const uint8_t *lds_qs,
+                                             const int16_t *lds_bs, const float *lds_d, Acc<NC> &acc) {
+    compute_item_ops<NC>(it, u, [&](int col) { return act_ops<F>(lds_qs, lds_bs, lds_d, cb0 + col * nb, u); }, acc);
 }
 
 // Item loads a lane keeps in flight while it computes: the lane walks its items through a ring of
@@ -435,23 +467,27 @@ __device__ __forceinline__ void gemv_rows_m(const uint8_t *const (&ws)[M], int n
 
 // The same stream for a matrix of contiguous rows whose row bytes are a multiple of 16, through LDS: a
 // wave pass (64 / LPR whole rows, at most GEMV_DMA_SLOT bytes) goes global -> LDS in 1 KB wave loads
-// (buffer_load_dwordx4 ... lds, non-temporal) into one of NS slots private to the wave, NS - 1 passes
-// ahead of the one being computed, and every lane then reads its items from the slot. Each cache line
-// of the matrix is fetched by one wave load and no register holds data in flight. A wave reads only
-// what it loaded itself: no barrier, only its own load counter: every fill issues the same
+// (buffer_load_dwordx4 ... lds, non-temporal) into one of NS slots private to the wave, and every lane
+// then reads its items from the slot. Each cache line of the matrix is fetched by one wave load and no
+// register holds data in flight. All NS slots are filled before the activations are staged (a wave of a
+// small matrix, two passes on the 4096 x 4096 Q4_K GEMV, then has every byte it reads in flight from
+// its start), and the slot of each computed pass is refilled with the pass NS ahead of it. A wave
+// reads only what it loaded itself: no barrier, only its own load counter: every fill issues the same
 // GEMV_DMA_SLOT / 1 KB wave loads, branch-free (lanes past the pass, and fills past the last pass, take
 // an offset beyond the buffer's range, which loads nothing), so a pass's fill is complete once at most
-// the loads of the NS - 1 fills issued after it are in flight, and the pass waits for exactly that. The slots are
-// distinct LDS arrays and the loop is unrolled NS times, so that every slot address is a constant.
-// (Buffer loads, not global ones: the compiler makes every LDS read after a global_load_lds wait for
-// all loads in flight.)
+// the loads of the NS - 1 fills issued after it are in flight, and the pass waits for exactly that. The
+// slots are distinct LDS arrays and the loop is unrolled NS times, so that every slot address is a
+// constant. (Buffer loads, not global ones: the compiler makes every LDS read after a global_load_lds
+// wait for all loads in flight.) pre() runs before the first fill is issued: it issues loads whose
+// results stage() uses (the activation floats), so that they return ahead of the weight bytes.
 constexpr int GEMV_DMA_SLOT = 4096;
 constexpr int GEMV_DMA_STASH = 256;  // floats of row totals per wave
 
-template <int F, int NC, int LPR, int NS, class Stage, class Store>
+template <int F, int NC, int LPR, int NS, class Pre, class Stage, class Store>
 __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int nb, int wave, int nwaves,
                                               uint8_t *const (&slots)[NS], float *stash, const uint8_t *lds_qs,
-                                              const int16_t *lds_bs, const float *lds_d, Stage stage, Store store) {
+                                              const int16_t *lds_bs, const float *lds_d, Pre pre, Stage stage,
+                                              Store store) {
     constexpr int FILL = GEMV_DMA_SLOT / 1024;  // wave loads per slot fill
     static_assert(GEMV_DMA_SLOT % 1024 == 0 && NS >= 2 && FILL * (NS - 1) < 64, "slots");
     constexpr int G = LPR / LPB;   // super-blocks of a row per wave pass
@@ -479,17 +515,33 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
         }
     };
     const bool active = wave < npass;  // uniform over the wave
-    if (active) {
+    pre();
+    // branch-free (a wave without passes issues fills that load nothing), so that the compiler's count
+    // of the loads in flight is the same on every path and stage() waits only for pre()'s loads
 #pragma unroll
-        for (int s = 0; s < NS - 1; ++s) dma(slots[s], wave + s * nwaves);
-    }
+    for (int s = 0; s < NS; ++s) dma(slots[s], wave + s * nwaves);
     stage();
-    if (!active) return;
+    if (!active) {
+        __builtin_amdgcn_s_waitcnt(0);  // the empty fills end before the wave does
+        return;
+    }
     // Row totals wait in the wave's stash until it is full or the stream ends: a store among the loads
     // would make the compiler wait for every load in flight (it cannot order the two kinds of access).
+    // A window holds the first pass (computed before the loop) and WINDOW_STEPS steps of NS passes.
     constexpr int STASH_PASSES = GEMV_DMA_STASH / (RPW * NC);
-    static_assert(STASH_PASSES >= NS, "stash of at least one unrolled step");
+    constexpr int WINDOW_STEPS = (STASH_PASSES - 1) / NS;
+    static_assert(WINDOW_STEPS >= 1, "stash of at least one unrolled step");
     int k = 0;
+    // A lane whose row part is one super-block (BPL = 1: the head and the 4096 x 4096 Q4_K GEMV) meets the
+    // same activation operands in every pass: with up to two columns they are read from LDS once, here,
+    // and held in registers, off the path from a pass's data to its totals.
+    constexpr int NH = NC <= 2 ? NC : 1;
+    const bool hold = NC <= 2 && BPL == 1;
+    ActOps held[NH];
+    if (hold) {
+#pragma unroll
+        for (int c = 0; c < NH; ++c) held[c] = act_ops<F>(lds_qs, lds_bs, lds_d, min(gb, nb - 1) + c * nb, u);
+    }
     auto pass = [&](const uint8_t *slot, int p) {
         __builtin_amdgcn_s_waitcnt(WAIT_FILL);
         asm volatile("" ::: "memory");
@@ -505,7 +557,11 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
             it.valid = row < nrows && b < nb;
             // an invalid item reads the pass's first block, which the pass always holds
             it.load(slot, it.valid ? (uint32_t)lrow * rb + (uint32_t)(b * BYTES) : 0u, u);
-            compute_item<NC>(it, u, min(b, nb - 1), nb, lds_qs, lds_bs, lds_d, acc);
+            if (hold) {
+                compute_item_ops<NC>(it, u, [&](int col) { return held[col < NH ? col : 0]; }, acc);
+            } else {
+                compute_item<NC>(it, u, min(b, nb - 1), nb, lds_qs, lds_bs, lds_d, acc);
+            }
         }
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc.v[c] = group_sum<LPR>(acc.v[c]);
@@ -523,16 +579,25 @@ __device__ __forceinline__ void gemv_rows_dma(const uint8_t *w, int nrows, int n
         }
         k = 0;
     };
-    // Windows of up to STASH_PASSES passes, NS at a time; the stores of a window's totals come after its
-    // loop and are waited for before the next window's, which therefore starts with no store pending.
-    for (int p = wave;;) {
+    // The first pass, from slot 0; then, pass by pass in slot order 1, 2, .., NS - 1, 0, 1, .., the slot of
+    // the pass just computed is refilled with the pass NS - 1 ahead of the next one before that one waits
+    // for its own fill (the order in which the compiler's count of the fills stays exact across the loop's
+    // back edge; refilling a slot right after its pass made it wait for every fill before one of the
+    // unrolled passes). The stores of a window's totals come after its loop and are waited for before
+    // the next window's, which therefore starts with no store pending.
+    int p = wave;
+    for (bool first = true;; first = false) {
         const int p0 = p;
         bool done = false;
-        for (int it = 0; it < STASH_PASSES / NS && !done; ++it) {
+        if (first) {
+            pass(slots[0], p);
+            done = (p += nwaves) >= npass;
+        }
+        for (int it = 0; it < WINDOW_STEPS && !done; ++it) {
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                dma(slots[(s + NS - 1) % NS], p + (NS - 1) * nwaves);
-                pass(slots[s], p);
+                dma(slots[s], p + (NS - 1) * nwaves);
+                pass(slots[(s + 1) % NS], p);
                 if ((p += nwaves) >= npass) {
                     done = true;
                     break;

@@ -134,7 +134,7 @@ __device__ __forceinline__ void mmid_pass(const MmidArgs &a, const uint8_t *w, c
             }
             col_dst[threadIdx.x] = off;
         }
-        __syncthreads();
+        lds_barrier();  // the weight loads issued before the staging stay in flight
     };
     float *dst = a.dst;
     gemv_rows<F, NC, LPR>(w, a.nrows, nb, (uint32_t)a.w_s1, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
@@ -224,7 +224,7 @@ __device__ __forceinline__ void expert_columns(const uint8_t *w, int nrows, int 
                 if ((int)threadIdx.x < n) dst_off(c0 + (int)threadIdx.x, off, sc);
                 col_dst[threadIdx.x] = off, col_scale[threadIdx.x] = sc;
             }
-            __syncthreads();
+            lds_barrier();  // the weight loads issued before the staging stay in flight
         };
         gemv_rows<F, NC, LPR>(w, nrows, nb, row_stride, blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6),
                               gridDim.x * GEMV_WAVES, lds_qs, lds_bs, lds_d, pre, [&](int c, int row, float v) {
