@@ -20,7 +20,11 @@
  *     case; tq_last_error() says which), -2 allocation failed;
  *   - the workspace is caller-provided device memory of at least the size the matching
  *     *_workspace_size() reports (a graph-capture-safe arena); workspace == NULL makes the library use
- *     a grow-only per-device buffer of its own (allocates on growth, so not capture-safe).
+ *     a grow-only buffer of its own per device and stream (allocates on growth, so not capture-safe);
+ *   - calls on different streams may run at once (each with its own workspace and outputs): the
+ *     counters through which the workgroups of some kernels meet (k split, router, single-launch MoE
+ *     step) belong to the issuing stream, up to 32 streams per device (a further stream's such call
+ *     fails); a captured graph keeps its capturing stream's counters.
  *
  * There is no CPU fallback inside this library: an unsupported case returns -1 and the caller keeps
  * ggml's own backend for it, as ggml's supports_op contract does.
@@ -180,9 +184,10 @@ int tq_copy_expert_slots(const tq_tensor *src, const tq_tensor *dst, int n_tenso
 /* Failed cross-workgroup waits of the single-launch MoE step (tq_moe_ffn up to 256 slots) on the current
  * device since the last clear: *count gets the error word (0: none), clear != 0 resets it. The step's
  * workgroups wait for each other with bounded polls; a wait that runs out (only possible when the GPU
- * cannot hold all of the launch's workgroups at once) leaves that call's outputs undefined. Synchronous
- * (reads device memory). No reference counterpart: ggml's CUDA MUL_MAT_ID runs its nodes as separate
- * launches. */
+ * cannot hold all of the launch's workgroups at once) writes NaN into the output rows of the workgroup
+ * that gave up, so the failure also reaches the caller's checks downstream. Synchronous (reads device
+ * memory): call it where the host synchronizes anyway. No reference counterpart: ggml's CUDA MUL_MAT_ID
+ * runs its nodes as separate launches. */
 int tq_moe_ffn_sync_errors(unsigned *count, int clear);
 
 /* Dequantize n elements of type (Q4_K, Q6_K or Q8_K; n a multiple of 256) from src to F32 dst.

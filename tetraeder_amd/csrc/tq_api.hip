@@ -64,29 +64,39 @@ int resident_waves_per_cu(const void *kernel, int threads, size_t lds) {
     return w;
 }
 
-// Grow-only per-device workspace for callers that pass none (allocates on growth: not capture-safe).
-static void *own_workspace(size_t bytes, int *rc) {
+// Grow-only workspace per device and stream for callers that pass none (allocates on growth: not
+// capture-safe). Calls on one stream run in order, so they can share it; other streams get their own.
+static void *own_workspace(size_t bytes, hipStream_t stream, int *rc) {
     static std::mutex mu;
-    static void *buf[MAX_DEVICES] = {nullptr};
-    static size_t cap[MAX_DEVICES] = {0};
+    static std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> bufs;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
         *rc = fail(TQ_STATUS_FAILED, "no current HIP device");
         return nullptr;
     }
     std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] < bytes) {
-        if (buf[dev]) (void)hipFree(buf[dev]);  // hipFree waits for work that still uses the old buffer
-        buf[dev] = nullptr;
-        cap[dev] = 0;
-        if (hipMalloc(&buf[dev], bytes) != hipSuccess) {
+    auto &b = bufs[std::make_pair(dev, stream)];
+    if (b.second < bytes) {
+        if (b.first) (void)hipFree(b.first);  // hipFree waits for work that still uses the old buffer
+        b.first = nullptr;
+        b.second = 0;
+        if (hipMalloc(&b.first, bytes) != hipSuccess) {
             *rc = fail(TQ_STATUS_ALLOC_FAILED, "workspace of %zu bytes", bytes);
             return nullptr;
         }
-        cap[dev] = bytes;
+        b.second = bytes;
     }
     *rc = TQ_STATUS_SUCCESS;
-    return buf[dev];
+    return b.first;
+}
+
+// The stream's counter block (SyncCounters) for kernels whose workgroups count or wait for each other.
+static SyncCounters *stream_counters(hipStream_t stream, int *rc) {
+    SyncCounters *c = sync_counters(stream);
+    *rc = c ? TQ_STATUS_SUCCESS
+            : fail(TQ_STATUS_FAILED, "no counter block for this stream: %d streams of this device already hold one",
+                   SYNC_STREAMS);
+    return c;
 }
 
 static bool is_weight(int t) { return t == TQ_TYPE_Q4_K || t == TQ_TYPE_Q6_K; }
@@ -292,7 +302,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         const size_t need = q8_need + split_need;
         if (workspace && workspace_size < need)
             return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, (hipStream_t)stream, &rc));
         if (!ws) return rc;
     }
     if (!pre_quantized && !in_wg) {
@@ -323,6 +333,11 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         if (split_need) {
             m.ksplit = mmq_tile_split(a->type, m.ncols, m.nrows, nb, m.nbatch);
             m.part = (float *)(ws + q8_need);
+            if (m.ksplit > 1) {
+                SyncCounters *sc = stream_counters(s, &rc);
+                if (!sc) return rc;
+                m.arrivals = sc->tiles;
+            }
         }
         if (skinny) return check_hip(launch_skinny(a->type, m, s), "skinny launch");
         return check_hip(launch_mmq(a->type, m, s), "mmq launch");
@@ -406,7 +421,7 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
         return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
     uint8_t *ws = nullptr;
     if (need) {
-        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+        ws = (uint8_t *)(workspace ? workspace : own_workspace(need, (hipStream_t)stream, &rc));
         if (!ws) return rc;
     }
     hipStream_t s = (hipStream_t)stream;
@@ -524,14 +539,18 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
     const size_t need = moe_workspace(gate, b, ids);
     if (workspace && workspace_size < need)
         return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, (hipStream_t)stream, &rc));
     if (!ws) return rc;
     hipStream_t s = (hipStream_t)stream;
     float *gu = (float *)ws;
     if (n_slots <= mmid_small_max_slots()) {
-        const MoeArgs m = moe_args(gate, up, down, b, ids, weights, dst, gu);
-        if (moe_fused_supported(gate->type, up->type, m))
+        MoeArgs m = moe_args(gate, up, down, b, ids, weights, dst, gu);
+        if (moe_fused_supported(gate->type, up->type, m)) {
+            SyncCounters *sc = stream_counters(s, &rc);
+            if (!sc) return rc;
+            m.done = sc->moe_done, m.exit_count = &sc->moe_exit;
             return check_hip(launch_moe_fused(gate->type, down->type, m, 0, s), "moe_ffn launch");
+        }
         return check_hip(launch_moe_ffn(gate->type, up->type, down->type, m, s), "moe_ffn launch");
     }
     // Many tokens: the same nodes composed, MUL_MAT_ID with device routing and elementwise glue.
@@ -570,7 +589,7 @@ int tq_moe_ffn_sum(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *
     const size_t need = moe_sum_workspace(gate, b, ids), base = moe_workspace(gate, b, ids);
     if (workspace && workspace_size < need)
         return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, &rc));
+    uint8_t *ws = (uint8_t *)(workspace ? workspace : own_workspace(need, (hipStream_t)stream, &rc));
     if (!ws) return rc;
     // the slot rows as a contiguous [n_embd, n_used, T] tensor in the workspace
     tq_tensor so{};
@@ -649,7 +668,7 @@ int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_
     const size_t need = tq_moe_router_workspace_size(gate_inp, ffn_inp);
     if (workspace && workspace_size < need)
         return fail(TQ_STATUS_FAILED, "workspace of %zu bytes, %zu needed", workspace_size, need);
-    float *ws = (float *)(workspace ? workspace : own_workspace(need, &rc));
+    float *ws = (float *)(workspace ? workspace : own_workspace(need, (hipStream_t)stream, &rc));
     if (!ws) return rc;
     RouterArgs a{};
     a.x = (const float *)ffn_inp->data, a.x_s1 = (int64_t)(ffn_inp->nb[1] / 4);
@@ -661,6 +680,11 @@ int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_
     a.logits = ws;
     a.ids = (int32_t *)ids->data, a.ids_s0 = (int64_t)(ids->nb[0] / 4), a.ids_s1 = (int64_t)(ids->nb[1] / 4);
     a.w = (float *)weights->data, a.w_s1 = (int64_t)(weights->nb[1] / 4), a.w_s2 = (int64_t)(weights->nb[2] / 4);
+    if (T <= SYNC_ROUTER_WORDS) {
+        SyncCounters *sc = stream_counters((hipStream_t)stream, &rc);
+        if (!sc) return rc;
+        a.arrive = sc->router;
+    }
     return check_hip(launch_router(a, (hipStream_t)stream), "router launch");
 }
 

@@ -9,6 +9,25 @@
 
 namespace tq {
 
+// Counters of the kernels whose workgroups count or wait for each other: the k split's tile arrivals,
+// the router's token arrivals and the MoE step's phase counts. Each stream that issues such a call gets
+// a block of its own from a file-scope device array (zero when the module loads; every call leaves the
+// counters it used at zero), so calls in flight on different streams of one GPU never share a counter
+// and nothing is allocated (graph capture records the capturing stream's block).
+constexpr int SYNC_TILE_WORDS = 8192;    // k split: output tiles (all batches) of one launch
+constexpr int SYNC_ROUTER_WORDS = 4096;  // router: tokens of one launch
+constexpr int SYNC_MOE_WORDS = 256;      // MoE step: routed experts of one launch
+struct SyncCounters {
+    unsigned tiles[SYNC_TILE_WORDS];
+    unsigned router[SYNC_ROUTER_WORDS];
+    unsigned moe_done[SYNC_MOE_WORDS];
+    unsigned moe_exit;
+    unsigned pad[63];
+};
+constexpr int SYNC_STREAMS = 32;  // streams per device that can hold a block
+// The block of `stream` on the current device; nullptr when SYNC_STREAMS other streams hold one.
+SyncCounters *sync_counters(hipStream_t stream);
+
 // Q8_K quantization of rows of k floats. Row r = (i3*ne2 + i2)*ne1 + i1 is read at
 // x + i1*s1 + i2*s2 + i3*s3 (byte strides) and written contiguously at y + r*(k/256)*292.
 hipError_t launch_quantize_q8_K(const void *x, int64_t k, int64_t ne1, int64_t ne2, int64_t ne3, size_t s1, size_t s2,
@@ -57,6 +76,7 @@ struct MmqArgs {
     int64_t d_s1, d_s2, d_s3;  // float strides
     int32_t ksplit;      // tile kernels: workgroups per output tile along k (1: none)
     float *part;         // ksplit > 1: workspace of mmq_split_bytes for the partial tiles
+    unsigned *arrivals;  // ksplit > 1: the tiles' arrival counts (the stream's SyncCounters::tiles)
 };
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 // The large-tile prefill kernel (128 x 256 tiles, LDS-DMA staging); launch_mmq takes it when supported.
@@ -117,6 +137,7 @@ struct MoeArgs {
     float *gu;                         // workspace: gate then up outputs, [2][n_slots][n_ff]
     float *dst;                        // [n_embd, n_used, T]
     int64_t o_s1, o_s2;                // floats
+    unsigned *done, *exit_count;       // single launch: per-expert phase counts and the exit count
 };
 hipError_t launch_moe_ffn(int type_gate, int type_up, int type_down, const MoeArgs &m, hipStream_t stream);
 // The whole step as one launch (one workgroup per CU, phases ordered by device-scope counters) when
@@ -162,6 +183,7 @@ struct RouterArgs {
     int64_t ids_s0, ids_s1;
     float *w;             // weight j of token t at w[j*w_s1 + t*w_s2]
     int64_t w_s1, w_s2;
+    unsigned *arrive;     // per-token arrival counts of the one-launch router (SyncCounters::router)
 };
 hipError_t launch_router(const RouterArgs &a, hipStream_t stream);
 

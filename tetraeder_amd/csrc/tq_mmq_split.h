@@ -3,17 +3,16 @@
 // its partial tile to the workspace with device-coherent stores, waits for them to complete and adds one
 // to the tile's arrival count; the last to arrive reads the other partials back and sums all S in split
 // order (the same order whoever arrives last: the result does not depend on timing), stores the tile and
-// resets the count for the next call. The counts live in a file-scope device array of each kernel's
-// source (zero when the module loads). Calls that overlap on one GPU would share them and must not be
-// issued (the reference issues from one thread on one stream).
+// resets the count for the next call. The counts are the issuing stream's SyncCounters::tiles.
 #pragma once
 
 #include "tq_device.h"
+#include "tq_internal.h"
 
 namespace tq {
 
 constexpr int MMQ_MAX_SPLIT = 4;
-constexpr int MMQ_MAX_SPLIT_TILES = 8192;  // output tiles (all batches) a split launch may have
+constexpr int MMQ_MAX_SPLIT_TILES = SYNC_TILE_WORDS;  // output tiles (all batches) a split launch may have
 
 // tile and split of this workgroup: N = ntiles * S ids dealt round robin over the 8 XCDs, remapped so
 // that consecutive ids (the tiles of one split, in order) run on one XCD when N allows

@@ -67,8 +67,6 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *
 // consecutive rows 8 distinct slots (32 banks).
 __device__ __forceinline__ int bkey(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// arrival counts of the k split's output tiles
-__device__ unsigned g_tile_q4k_arrivals[MMQ_MAX_SPLIT_TILES];
 
 }  // namespace
 
@@ -306,7 +304,7 @@ __global__ __launch_bounds__(TL_THREADS, 1) void k_mmq_tile_q4k(MmqArgs a) {
                 for (int i = 0; i < 16; ++i) v[(fm * TL_FN + fn) * 16 + i] = acc[fm][fn][i];
         const int gt = blockIdx.y * ntiles + t;
         if (!mmq_split_reduce<TL_FM * TL_FN * 16, TL_THREADS>(v, a.part + (int64_t)gt * S * TL_TM * TL_TN, split, S,
-                                                              &g_tile_q4k_arrivals[gt], &arrival))
+                                                              &a.arrivals[gt], &arrival))
             return;
 #pragma unroll
         for (int fm = 0; fm < TL_FM; ++fm)
@@ -345,7 +343,7 @@ hipError_t launch_mmq_tile(int type, const MmqArgs &a, hipStream_t stream) {
     const int64_t tiles = (int64_t)((a.ncols + TL_TM - 1) / TL_TM) * ((a.nrows + TL_TN - 1) / TL_TN);
     const int S = a.ksplit > 1 ? a.ksplit : 1;
     if (tiles * S > 0x7fffffff) return hipErrorInvalidValue;
-    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
+    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || !a.arrivals || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
         return hipErrorInvalidValue;
     k_mmq_tile_q4k<<<dim3((unsigned)(tiles * S), (unsigned)a.nbatch), TL_THREADS, 0, stream>>>(a);
     return hipGetLastError();

@@ -49,8 +49,6 @@ static_assert(T6_TM == 128 && T6_TN == 128, "the k split's tile shape (mmq_tile_
 // (distinct banks of a 64-bank LDS at a 128-byte pitch) and 8 aligned consecutive rows 8 distinct slots
 __device__ __forceinline__ int rkey(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// arrival counts of the k split's output tiles
-__device__ unsigned g_tile_q6k_arrivals[MMQ_MAX_SPLIT_TILES];
 
 }  // namespace
 
@@ -265,7 +263,7 @@ __global__ __launch_bounds__(T6_THREADS, 1) void k_mmq_tile_q6k(MmqArgs a) {
             for (int i = 0; i < 16; ++i) v[fm * 16 + i] = acc[fm][i];
         const int gt = blockIdx.y * ntiles + t;
         if (!mmq_split_reduce<T6_FM * 16, T6_THREADS>(v, a.part + (int64_t)gt * S * T6_TM * T6_TN, split, S,
-                                                      &g_tile_q6k_arrivals[gt], &arrival))
+                                                      &a.arrivals[gt], &arrival))
             return;
 #pragma unroll
         for (int fm = 0; fm < T6_FM; ++fm)
@@ -298,7 +296,7 @@ hipError_t launch_mmq_tile_q6k(const MmqArgs &a, hipStream_t stream) {
     const int64_t tiles = (int64_t)((a.ncols + T6_TM - 1) / T6_TM) * ((a.nrows + T6_TN - 1) / T6_TN);
     const int S = a.ksplit > 1 ? a.ksplit : 1;
     if (tiles * S > 0x7fffffff) return hipErrorInvalidValue;
-    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
+    if (S > 1 && (S > MMQ_MAX_SPLIT || S > a.nb || !a.part || !a.arrivals || tiles * a.nbatch > MMQ_MAX_SPLIT_TILES))
         return hipErrorInvalidValue;
     k_mmq_tile_q6k<<<dim3((unsigned)(tiles * S), (unsigned)a.nbatch), T6_THREADS, 0, stream>>>(a);
     return hipGetLastError();

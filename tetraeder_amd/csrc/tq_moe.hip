@@ -23,12 +23,12 @@
 // Slots whose id is outside [0, n_expert) read no weights and get exact zero rows (patch 0004,
 // patches/0004-cuda-mul-mat-id-skip-negative.patch:116-137,214-253).
 //
-// The completion counts live in file-scope device counters (zero when the module loads): done[a] for
-// routed expert a, exit for the workgroups that finished the call; the last workgroup to finish resets
-// them, so every call starts from zero. Calls that overlap on one GPU (two streams) would share the
-// counters and must not be issued (the reference issues from one thread on one stream). Every wait is
-// bounded: past spin_limit polls a workgroup stops waiting, records the failure in the error word (read
-// with tq_moe_ffn_sync_errors) and that call's outputs are undefined, but every wave still exits.
+// The completion counts are the issuing stream's (SyncCounters::moe_done / moe_exit, zero when the module
+// loads): done[a] for routed expert a, exit for the workgroups that finished the call; the last workgroup
+// to finish resets them, so every call starts from zero, and calls on other streams use other counters.
+// Every wait is bounded: past spin_limit polls a workgroup stops waiting, records the failure in the
+// error word (read with tq_moe_ffn_sync_errors) and writes NaN into the rows it owns, and every wave still
+// exits.
 #include "tq_gemv_core.h"
 #include "tq_internal.h"
 
@@ -38,12 +38,12 @@
 namespace tq {
 
 constexpr int MOE_THREADS = GEMV_WAVES * 64;
-constexpr int MOE_MAX_SLOTS = 256;
+constexpr int MOE_MAX_SLOTS = SYNC_MOE_WORDS;
 constexpr int MOE_MAX_EXPERTS = 1024;
 constexpr int MOE_NC = 4;  // columns per staged pass (more columns take more passes)
 
-__device__ unsigned int g_moe_done[MOE_MAX_SLOTS];
-__device__ unsigned int g_moe_exit;
+// Failed bounded waits on this device (sticky; read and cleared by moe_sync_errors). The phase counts are
+// the issuing stream's (MoeArgs::done, exit_count).
 __device__ unsigned int g_moe_error;
 
 struct MoeRoute {
@@ -247,6 +247,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
     __shared__ int first[MOE_MAX_SLOTS + 1];
     __shared__ int cls[2 * MOE_MAX_SLOTS];
     __shared__ int mine;
+    __shared__ int wait_failed;  // the phase-2 wait ran out: this workgroup's rows become NaN
     __shared__ int64_t col_off[MOE_NC];
     __shared__ float col_scale[MOE_NC];
     extern __shared__ __align__(16) uint8_t lds[];
@@ -294,7 +295,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
         // publish: this workgroup's act stores are complete (device-coherent) before its count is added
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_fetch_add(&g_moe_done[a], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(&m.done[a], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
         // ---------------- phase 2: down rows of expert a ----------------
         const int nb2 = m.n_ff / QK;
@@ -322,9 +323,11 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
                     if (threadIdx.x == 0) {
                         const unsigned target = (unsigned)nk;
                         unsigned polls = 0;
-                        while (__hip_atomic_load(&g_moe_done[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                        wait_failed = 0;
+                        while (__hip_atomic_load(&m.done[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
                             if (++polls > spin_limit) {
                                 __hip_atomic_fetch_or(&g_moe_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                wait_failed = 1;
                                 break;
                             }
                             __builtin_amdgcn_s_sleep(2);
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
                     // this workgroup reads no counter after its wait: it counts itself out now, so the
                     // atomic's round trip overlaps the down rows
                     if (threadIdx.x == 0)
-                        exit_prev = __hip_atomic_fetch_add(&g_moe_exit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        exit_prev = __hip_atomic_fetch_add(m.exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
                 // act of each slot, quantized to Q8_K block by block, one wave per block
                 for (int i = wave; i < n * nb2; i += GEMV_WAVES) {
@@ -353,7 +356,9 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
             float *dst = m.dst + p0 * RPW2;
             gemv_rows<FD, NC, LPR2>(dw, nrows2, nb2, (uint32_t)m.dn_s1, wave, GEMV_WAVES, lds_qs, lds_bs, lds_d, stage,
                                     [&](int c, int row, float v) {
-                                        if (c < n) dst[col_off[c] + row] = v * col_scale[c];
+                                        // rows computed from an act that was not complete read NaN, so the
+                                        // failure reaches the caller's checks downstream
+                                        if (c < n) dst[col_off[c] + row] = wait_failed ? __builtin_nanf("") : v * col_scale[c];
                                     });
         });
     }
@@ -369,10 +374,10 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_fused(MoeArgs m, unsigned s
     // the next call
     if (threadIdx.x == 0) {
         if (!counted)
-            exit_prev = __hip_atomic_fetch_add(&g_moe_exit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            exit_prev = __hip_atomic_fetch_add(m.exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (exit_prev == gridDim.x - 1) {
-            for (int i = 0; i < n_act; ++i) __hip_atomic_store(&g_moe_done[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&g_moe_exit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < n_act; ++i) __hip_atomic_store(&m.done[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(m.exit_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

@@ -9,9 +9,8 @@
 //   then the last of a token's workgroups to finish (a device arrival count per token) takes one wave
 //     through softmax (the exponentials summed in double), the n_used largest probabilities, largest
 //     first, ties to the lower expert id (n_used rounds of a whole-wave maximum), and their normalized
-//     weights. Above ROUTER_FUSED_MAX_TOK
-//     tokens that is a second launch (k_router_topk). Calls that overlap on one GPU would share the
-//     counts and must not be issued.
+//     weights. Above ROUTER_FUSED_MAX_TOK tokens that is a second launch (k_router_topk). The counts are
+//     the issuing stream's SyncCounters::router.
 #include "tq_device.h"
 #include "tq_internal.h"
 
@@ -21,7 +20,7 @@ namespace tq {
 
 constexpr int ROUTER_THREADS = 256;
 constexpr int ROUTER_WAVES = 4;  // waves per logits workgroup; a slice is ROUTER_WAVES * EPW experts
-constexpr int ROUTER_FUSED_MAX_TOK = 4096;  // tokens of a one-launch router call
+constexpr int ROUTER_FUSED_MAX_TOK = SYNC_ROUTER_WORDS;  // tokens of a one-launch router call
 constexpr int ROUTER_CHUNK = 2048;          // row elements whose loads are all issued up front
 constexpr int ROUTER_EPW1_MAX_TOK = 2;      // tokens up to which a wave takes one expert (measured: 4 and 8 are faster with two)
 
@@ -70,9 +69,8 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return (rd_d(v, 15) + rd_d(v, 31)) + (rd_d(v, 47) + rd_d(v, 63));
 }
 
-// Arrival counts of the fused launch: the last of a token's slice workgroups runs its top-k (the counts
-// live in device memory, zero when the module loads, and each last arriver resets its token's).
-__device__ unsigned g_router_arrive[ROUTER_FUSED_MAX_TOK];
+// Arrival counts of the fused launch (a.arrive): the last of a token's slice workgroups runs its top-k
+// and resets its token's count.
 
 template <int PER, bool FUSED, int EPW>
 __global__ __launch_bounds__(ROUTER_THREADS) void k_router_logits(RouterArgs a) {
@@ -164,13 +162,13 @@ __global__ __launch_bounds__(ROUTER_THREADS) void k_router_logits(RouterArgs a) 
         __shared__ unsigned prev;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) prev = __hip_atomic_fetch_add(&g_router_arrive[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) prev = __hip_atomic_fetch_add(&a.arrive[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (prev != gridDim.x - 1) return;
         if (wave == 0) {
             const float *l = a.logits + (int64_t)t * a.n_expert;
             router_topk<PER>(a, t, [&](int e) { return __hip_atomic_load(l + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); });
-            if (lane == 0) __hip_atomic_store(&g_router_arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) __hip_atomic_store(&a.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -241,7 +239,7 @@ static hipError_t launch_router_epw(const RouterArgs &a, hipStream_t stream) {
     constexpr int SLICE = ROUTER_WAVES * EPW;
     const dim3 g1((unsigned)((a.n_expert + SLICE - 1) / SLICE), (unsigned)a.ntok);
     const size_t lds = (size_t)a.n_embd * sizeof(float);
-    if (a.ntok <= ROUTER_FUSED_MAX_TOK) {
+    if (a.ntok <= ROUTER_FUSED_MAX_TOK && a.arrive) {
         k_router_logits<PER, true, EPW><<<g1, ROUTER_THREADS, lds, stream>>>(a);
         return hipGetLastError();
     }
