@@ -101,6 +101,15 @@ size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b);
 int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
                void *stream);
 
+/* tq_mul_mat for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and results, with no workspace argument; the Q8_K
+ * copy of b and the k split's partial tiles go to a device array of the library, 32 MiB per GPU (held
+ * from the first call on a GPU until the process ends). Operands whose tq_mul_mat_workspace_size is
+ * above 32 MiB are rejected (-1). The array is shared by every call on a GPU: calls that overlap on one
+ * GPU (other streams, concurrent graphs) race and must not be issued. No counterpart in the reference
+ * (ggml's backend allocates its scratch from the context's pool); it exists for those callers. */
+int tq_mul_mat_noalloc(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *stream);
+
 /* Workspace bytes tq_mul_mat_id needs for these operands. */
 size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids);
 

@@ -28,6 +28,7 @@ _SIGNATURES = {
     "tq_mul_mat_workspace_size": ([C.POINTER(TqTensor), C.POINTER(TqTensor)], C.c_size_t),
     "tq_mul_mat": ([C.POINTER(TqTensor), C.POINTER(TqTensor), C.POINTER(TqTensor), C.c_void_p, C.c_size_t,
                     C.c_void_p], C.c_int),
+    "tq_mul_mat_noalloc": ([C.POINTER(TqTensor), C.POINTER(TqTensor), C.POINTER(TqTensor), C.c_void_p], C.c_int),
     "tq_mul_mat_id_workspace_size": ([C.POINTER(TqTensor), C.POINTER(TqTensor), C.POINTER(TqTensor)], C.c_size_t),
     "tq_mul_mat_id": ([C.POINTER(TqTensor), C.POINTER(TqTensor), C.POINTER(TqTensor), C.POINTER(TqTensor),
                        C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),

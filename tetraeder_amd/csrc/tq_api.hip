@@ -99,6 +99,37 @@ static SyncCounters *stream_counters(hipStream_t stream, int *rc) {
     return c;
 }
 
+// The scratch of tq_mul_mat_noalloc (the Q8_K copy of b and the k split's partial tiles): a file-scope
+// device array, so the entry point allocates nothing; each GPU the library runs on holds it until the
+// process ends. Every call on a GPU shares that GPU's array (calls that overlap on one GPU race).
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+// The device address of `scratch` on the current device, looked up once per device with that device
+// current (in host code the array's name is a host-side stand-in, not a device address).
+static uint8_t *scratch_address(int *rc) {
+    static std::mutex mu;
+    static uint8_t *ptr[MAX_DEVICES] = {nullptr};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        *rc = fail(TQ_STATUS_FAILED, "no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            *rc = fail(TQ_STATUS_FAILED, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        ptr[dev] = (uint8_t *)p;
+    }
+    *rc = TQ_STATUS_SUCCESS;
+    return ptr[dev];
+}
+
 static bool is_weight(int t) { return t == TQ_TYPE_Q4_K || t == TQ_TYPE_Q6_K; }
 
 static size_t type_size(int t) {
@@ -372,6 +403,21 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         if ((rc = check_hip(launch_gemv(a->type, g, s), "gemv launch"))) return rc;
     }
     return TQ_STATUS_SUCCESS;
+}
+
+int tq_mul_mat_noalloc(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *stream) {
+    int rc;
+    if ((rc = check_tensor(a, "a")) || (rc = check_tensor(b, "b"))) return rc;
+    const size_t need = tq_mul_mat_workspace_size(a, b);
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(TQ_STATUS_FAILED,
+                    "tq_mul_mat_noalloc: these operands need %zu bytes of scratch, its array holds %zu "
+                    "(call tq_mul_mat with a workspace)", need, NOALLOC_SCRATCH_BYTES);
+    uint8_t *ws = nullptr;
+    if (need && !(ws = scratch_address(&rc))) return rc;
+    // the kernels of tq_mul_mat, with the array as their workspace; nothing in it needs to start at zero
+    // (the Q8_K rows and every partial tile are written before they are read)
+    return tq_mul_mat(a, b, dst, ws, need ? NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 static int check_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, const tq_tensor *dst) {
