@@ -210,6 +210,76 @@ int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream);
  * every block is valid; for model conversion and synthetic weights, never on the matmul path. */
 int tq_quantize_weights(int type, const float *src, void *dst, int64_t nrows, int64_t n_per_row, void *stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * The backend module: the shape of a ggml backend module (ggml_backend_reg / ggml_backend_dev /
+ * ggml_backend, the registry the reference loads with ggml_backend_load_all_from_path at
+ * crates/ggml-sys/src/llama/mod.rs:191-231 and computes through with ggml_backend_graph_compute_async,
+ * crates/ggml-sys/src/ggml/backend.rs:262-278, issued by Executor::issue, crates/executor/src/exec.rs:258),
+ * over the operators above: a registry of the gfx950 devices, supports_op for a node, and a backend
+ * instance that runs a list of nodes in order on its stream out of one workspace arena sized by a
+ * reserve pass (ggml_backend_sched_reserve, crates/ggml-sys/src/ggml/sched.rs:63-77), so that a
+ * compute allocates nothing and can be captured into a HIP graph.
+ * ------------------------------------------------------------------------------------------------ */
+
+/* Node operators: ggml's MUL_MAT and MUL_MAT_ID, and the fused nodes of a Qwen3-MoE layer above. */
+enum tq_node_op {
+    TQ_NODE_MUL_MAT = 1,         /* src[0] a, src[1] b                                  -> dst[0] */
+    TQ_NODE_MUL_MAT_ID = 2,      /* src[0] as, src[1] b, src[2] ids                     -> dst[0] */
+    TQ_NODE_MOE_ROUTER = 3,      /* src[0] ffn_inp, src[1] ffn_norm, src[2] gate_inp, f_param eps,
+                                  * i_param n_used                       -> dst[0] xn, dst[1] weights, dst[2] ids */
+    TQ_NODE_MOE_FFN = 4,         /* src[0..2] gate/up/down exps, src[3] b, src[4] ids, src[5] weights
+                                  * or NULL                                               -> dst[0] slot rows */
+    TQ_NODE_MOE_FFN_SUM = 5,     /* as TQ_NODE_MOE_FFN                                   -> dst[0] [n_embd, T] */
+    TQ_NODE_SUM_EXPERTS = 6,     /* src[0] experts [n_embd, n_used, T]                   -> dst[0] [n_embd, T] */
+};
+
+/* One graph node: its operator, sources and destinations (struct ggml_tensor's op, src[] and the node
+ * itself) and its scalar parameters (ggml's op_params). Unused entries are NULL. */
+typedef struct tq_node {
+    int32_t op;
+    const tq_tensor *src[6];
+    tq_tensor *dst[3];
+    float f_param;
+    int32_t i_param;
+} tq_node;
+
+typedef struct tq_backend tq_backend;
+
+/* The registry's name ("TQ-HIP") and its devices: the HIP devices that are gfx950, in HIP's order
+ * (ggml_backend_reg_name, ggml_backend_reg_dev_count). */
+const char *tq_backend_reg_name(void);
+int tq_backend_dev_count(void);
+/* Device index i of the registry -> its HIP device ordinal, description ("<name> (<arch>), <n> CUs") and
+ * memory (ggml_backend_dev_description, ggml_backend_dev_memory). -1 when i is out of range. */
+int tq_backend_dev_hip_ordinal(int i);
+int tq_backend_dev_description(int i, char *buf, size_t len);
+int tq_backend_dev_memory(int i, size_t *free_bytes, size_t *total_bytes);
+
+/* 1 when the backend computes this node (operator, types and shapes), 0 when the scheduler must give it
+ * to another backend (ggml_backend_dev_supports_op); no device is touched. */
+int tq_backend_supports_node(const tq_node *node);
+
+/* A backend instance on registry device i issuing on `stream` (NULL: a stream of its own, created at
+ * default priority); NULL on failure (tq_last_error). ggml_backend_dev_init. */
+tq_backend *tq_backend_init(int i, void *stream);
+void tq_backend_free(tq_backend *backend);
+const char *tq_backend_name(tq_backend *backend);
+void *tq_backend_get_stream(tq_backend *backend);
+
+/* Sizes the backend's workspace arena for these nodes (the largest any one of them needs: the nodes run
+ * one after another on one stream) and allocates it if it grows; call outside graph capture. Fails
+ * (-1) on a node the backend does not support. ggml_backend_sched_reserve. */
+int tq_backend_reserve(tq_backend *backend, const tq_node *nodes, int n_nodes);
+
+/* Runs the nodes in order on the backend's stream (asynchronous; no host synchronization, no
+ * allocation: a node needing more workspace than the last reserve provided fails with -1 before
+ * anything of it is issued). Returns the ggml_status of the first node that fails, with its index in
+ * tq_last_error(). ggml_backend_graph_compute_async. */
+int tq_backend_graph_compute(tq_backend *backend, const tq_node *nodes, int n_nodes);
+
+/* Waits for the backend's stream (ggml_backend_synchronize). */
+int tq_backend_synchronize(tq_backend *backend);
+
 #ifdef __cplusplus
 }
 #endif

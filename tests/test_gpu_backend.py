@@ -1,0 +1,129 @@
+"""The backend module on the GPU: one decode layer of a Qwen3-MoE-shaped model (n_embd 2048, 128 experts,
+top-8) as a node list (attention projections q/k/v/o as MUL_MAT, the router, the expert FFN summed over
+slots, an output head as MUL_MAT), reserved once and computed on the backend's stream (the path of
+Sched::compute / Backend::compute_async, crates/ggml-sys/src/ggml/sched.rs:112, backend.rs:262). Every
+node's output equals the same entry point called on its own (bit for bit: the same kernels) and the
+MUL_MAT nodes match the oracle; the compute records into a HIP graph whose replays reproduce it; a node
+the backend does not take, or one needing more workspace than reserved, fails before anything of it
+is issued."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tetraeder_amd import backend as B, ggml
+from tests.helpers import normal
+from tests.test_gpu_mmid import make_experts
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name):
+    print(f"[backend] {name}", file=sys.stderr, flush=True)
+
+
+def make_weights(ty, k, n, seed, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    src = torch.randn((n, k), generator=g, device=device) * 0.02
+    return ggml.QTensor(ty, (k, n), ggml.quantize(ty, src, n, k))
+
+
+def layer(gpu, T):
+    n_embd, n_ff, E, vocab = 2048, 768, 128, 32000
+    W = {"q": make_weights(ggml.Type.Q4_K, n_embd, 4096, 1, gpu), "k": make_weights(ggml.Type.Q4_K, n_embd, 512, 2, gpu),
+         "v": make_weights(ggml.Type.Q4_K, n_embd, 512, 3, gpu), "o": make_weights(ggml.Type.Q4_K, 4096, n_embd, 4, gpu),
+         "head": make_weights(ggml.Type.Q6_K, n_embd, vocab, 5, gpu)}
+    gate = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=6, device=gpu)
+    up = make_experts(ggml.Type.Q4_K, n_embd, n_ff, E, seed=7, device=gpu)
+    down = make_experts(ggml.Type.Q6_K, n_ff, n_embd, E, seed=8, device=gpu)
+    gate_inp = torch.from_numpy((0.02 * np.random.default_rng(9).standard_normal((E, n_embd))).astype(np.float32)).to(gpu)
+    norm = torch.from_numpy((1 + 0.1 * np.random.default_rng(10).standard_normal(n_embd)).astype(np.float32)).to(gpu)
+    x = torch.from_numpy(normal((T, n_embd), 11)).to(gpu)
+    attn = torch.from_numpy(normal((T, 4096), 12)).to(gpu)
+    nq, nk, nv = B.mul_mat(W["q"], x), B.mul_mat(W["k"], x), B.mul_mat(W["v"], x)
+    no = B.mul_mat(W["o"], attn)
+    nr = B.moe_router(no.out, norm, gate_inp, 1e-6, 8)
+    xn, w, ids = nr.out
+    nm = B.moe_ffn_sum(gate, up, down, xn.view(T, 1, n_embd), ids, w)
+    nh = B.mul_mat(W["head"], nm.out)
+    nodes = [nq, nk, nv, no, nr, nm, nh]
+    return nodes, W, (gate, up, down, gate_inp, norm, x, attn)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_decode_layer_through_the_backend(gpu, T):
+    _case(f"layer T={T}")
+    assert B.Backend.gpu_count() >= 1
+    be = B.Backend.gpu(0)
+    assert "gfx950" in be.description()
+    nodes, W, (gate, up, down, gate_inp, norm, x, attn) = layer(gpu, T)
+    for n in nodes:
+        assert B.supports(n)
+    be.reserve(nodes)
+    be.compute_async(nodes)
+    be.synchronize()
+    nq, nk, nv, no, nr, nm, nh = nodes
+    # each node against its entry point called alone, on the node's own inputs
+    torch.cuda.synchronize()
+    for n, w, inp in ((nq, W["q"], x), (nk, W["k"], x), (nv, W["v"], x), (no, W["o"], attn), (nh, W["head"], nm.out)):
+        assert torch.equal(n.out, ggml.mul_mat(w, inp)), "MUL_MAT node differs from tq_mul_mat"
+    xn, wts, ids = ggml.moe_router(no.out, norm, gate_inp, 1e-6, 8)
+    assert torch.equal(nr.out[0], xn) and torch.equal(nr.out[1], wts) and torch.equal(nr.out[2], ids)
+    y = ggml.moe_ffn_sum(gate, up, down, nr.out[0].view(T, 1, -1), nr.out[2], nr.out[1])
+    assert torch.equal(nm.out, y), "MoE node differs from tq_moe_ffn_sum"
+    # the MUL_MAT nodes against the oracle
+    for n, w, inp in ((nq, W["q"], x), (no, W["o"], attn)):
+        want = O.mul_mat(w.type.id, w.data.cpu().numpy(), w.ne[0], w.ne[1], inp.cpu().numpy())[0]
+        got = n.out.cpu().numpy()
+        assert float(np.abs(got - want).max() / np.abs(want).max()) <= 1e-3
+    be.close()
+
+
+def test_backend_compute_in_a_graph(gpu):
+    """A reserved compute records into a HIP graph (nothing allocated, no host synchronization); three
+    replays, with the outputs poisoned and other work on the stream between them, equal the eager run."""
+    _case("graph capture")
+    T = 2
+    nodes, W, _ = layer(gpu, T)
+    be = B.Backend.gpu(0)
+    be.reserve(nodes)
+    be.compute_async(nodes)
+    be.synchronize()
+    eager = [[t.clone() for t in (n.dsts)] for n in nodes]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=be.stream):
+        be.compute_async(nodes)
+    for rep in range(3):
+        for n in nodes:
+            for t in n.dsts:
+                t.fill_(-7 if t.dtype == torch.int32 else float("nan"))
+        ggml.mul_mat(W["q"], torch.randn((3, 2048), device=gpu))  # other work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for n, ref in zip(nodes, eager):
+            for t, r in zip(n.dsts, ref):
+                assert torch.equal(t, r), f"replay {rep}: node op {n.op} differs from the eager compute"
+    be.close()
+
+
+def test_backend_refusals(gpu):
+    _case("refusals")
+    be = B.Backend.gpu(0)
+    w = make_weights(ggml.Type.Q4_K, 2048, 512, 21, gpu)
+    small = B.mul_mat(w, torch.randn((1, 2048), device=gpu))
+    big = B.mul_mat(w, torch.randn((300, 2048), device=gpu))  # needs a Q8_K copy in the workspace
+    be.reserve([small])
+    with pytest.raises(ggml.Compute, match="node 1"):
+        be.compute_async([small, big])
+    bad = B.mul_mat(w, torch.randn((1, 1024), device=gpu))
+    with pytest.raises(ggml.Compute, match="not supported"):
+        be.reserve([small, bad])
+    be.reserve([small, big])
+    be.compute_async([small, big])
+    be.synchronize()
+    assert torch.equal(big.out, ggml.mul_mat(w, big.srcs[1]))
+    be.close()

@@ -44,7 +44,27 @@ _SIGNATURES = {
     "tq_moe_ffn_sync_errors": ([C.POINTER(C.c_uint), C.c_int], C.c_int),
     "tq_to_f32": ([C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p], C.c_int),
     "tq_quantize_weights": ([C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p], C.c_int),
+    "tq_backend_reg_name": ([], C.c_char_p),
+    "tq_backend_dev_count": ([], C.c_int),
+    "tq_backend_dev_hip_ordinal": ([C.c_int], C.c_int),
+    "tq_backend_dev_description": ([C.c_int, C.c_char_p, C.c_size_t], C.c_int),
+    "tq_backend_dev_memory": ([C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)], C.c_int),
+    "tq_backend_supports_node": ([C.c_void_p], C.c_int),
+    "tq_backend_init": ([C.c_int, C.c_void_p], C.c_void_p),
+    "tq_backend_free": ([C.c_void_p], None),
+    "tq_backend_name": ([C.c_void_p], C.c_char_p),
+    "tq_backend_get_stream": ([C.c_void_p], C.c_void_p),
+    "tq_backend_reserve": ([C.c_void_p, C.c_void_p, C.c_int], C.c_int),
+    "tq_backend_graph_compute": ([C.c_void_p, C.c_void_p, C.c_int], C.c_int),
+    "tq_backend_synchronize": ([C.c_void_p], C.c_int),
 }
+
+
+class TqNode(C.Structure):
+    """struct tq_node (include/tq.h): operator, sources, destinations, scalar parameters."""
+
+    _fields_ = [("op", C.c_int32), ("src", C.POINTER(TqTensor) * 6), ("dst", C.POINTER(TqTensor) * 3),
+                ("f_param", C.c_float), ("i_param", C.c_int32)]
 
 
 def lib() -> C.CDLL:

@@ -15,8 +15,14 @@
 namespace tq {
 
 static thread_local std::string g_err;
+// Set while a node is only checked (supports_node): tensors may have no data yet, so their addresses
+// are neither required nor checked for alignment, as ggml's supports_op sees unallocated tensors.
+static thread_local bool g_shape_only = false;
 
-static int fail(int code, const char *fmt, ...) {
+// An address that breaks the alignment a kernel needs (never, while shapes alone are checked).
+static bool misaligned(const void *p, size_t align) { return !g_shape_only && (uintptr_t)p % align != 0; }
+
+int fail(int code, const char *fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -154,7 +160,7 @@ static int check_tensor(const tq_tensor *t, const char *name) {
     if (!t) return fail(TQ_STATUS_FAILED, "%s is NULL", name);
     for (int i = 0; i < 4; ++i)
         if (t->ne[i] < 0) return fail(TQ_STATUS_FAILED, "%s ne[%d] = %lld", name, i, (long long)t->ne[i]);
-    if (!t->data && nrows(t) * t->ne[0] > 0) return fail(TQ_STATUS_FAILED, "%s data is NULL", name);
+    if (!t->data && nrows(t) * t->ne[0] > 0 && !g_shape_only) return fail(TQ_STATUS_FAILED, "%s data is NULL", name);
     return TQ_STATUS_SUCCESS;
 }
 
@@ -168,7 +174,7 @@ static int check_weight_layout(const tq_tensor *a, const char *name) {
     // Q4_K rows are read as 16-byte words; Q6_K blocks (210 bytes) through the aligned dwords that hold
     // them, which needs 4-byte aligned matrices and even row strides.
     const size_t align = a->type == TQ_TYPE_Q4_K ? 16 : 4, row_align = a->type == TQ_TYPE_Q4_K ? 16 : 2;
-    if ((uintptr_t)a->data % align || a->nb[1] % row_align || (a->ne[2] > 1 && a->nb[2] % align) ||
+    if (misaligned(a->data, align) || a->nb[1] % row_align || (a->ne[2] > 1 && a->nb[2] % align) ||
         (a->ne[3] > 1 && a->nb[3] % align))
         return fail(TQ_STATUS_FAILED, "%s data, row stride and matrix strides must be %zu, %zu, %zu-byte aligned", name,
                     align, row_align, align);
@@ -183,7 +189,7 @@ static int check_f32(const tq_tensor *t, const char *name) {
     if (t->type != TQ_TYPE_F32) return fail(TQ_STATUS_FAILED, "%s type %d is not F32", name, t->type);
     if (t->nb[0] != 4 || t->nb[1] % 4 || t->nb[2] % 4 || t->nb[3] % 4)
         return fail(TQ_STATUS_FAILED, "%s must have contiguous float rows (nb[0] == 4)", name);
-    if ((uintptr_t)t->data % 4) return fail(TQ_STATUS_FAILED, "%s data is not float aligned", name);
+    if (misaligned(t->data, 4)) return fail(TQ_STATUS_FAILED, "%s data is not float aligned", name);
     return TQ_STATUS_SUCCESS;
 }
 
@@ -291,8 +297,8 @@ size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b) {
     return mul_mat_q8_part(a, b) + mul_mat_split_part(a, b);
 }
 
-int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
-               void *stream) {
+// ggml's shape rules for MUL_MAT and the limits of the kernels here.
+static int check_mul_mat(const tq_tensor *a, const tq_tensor *b, const tq_tensor *dst) {
     int rc;
     if ((rc = check_tensor(a, "a")) || (rc = check_tensor(b, "b")) || (rc = check_tensor(dst, "dst"))) return rc;
     if ((rc = check_weight_layout(a, "a")) || (rc = check_f32(dst, "dst"))) return rc;
@@ -302,7 +308,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     if (pre_quantized) {
         const size_t rs = row_size(TQ_TYPE_Q8_K, b->ne[0]);
         if (b->ne[0] % QK || b->nb[0] != Q8K_BYTES || b->nb[1] != rs || b->nb[2] != rs * b->ne[1] ||
-            b->nb[3] != rs * b->ne[1] * b->ne[2] || (uintptr_t)b->data % 4)
+            b->nb[3] != rs * b->ne[1] * b->ne[2] || misaligned(b->data, 4))
             return fail(TQ_STATUS_FAILED, "a Q8_K b must be contiguous 4-byte aligned blocks");
     } else if ((rc = check_f32(b, "b"))) {
         return rc;
@@ -314,13 +320,25 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     if (dst->ne[0] != a->ne[1] || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3])
         return fail(TQ_STATUS_FAILED, "dst shape is not [a.ne1, b.ne1, b.ne2, b.ne3]");
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
-    if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
     const int nb = (int)(a->ne[0] / QK);
     const bool mmq = use_mmq(a->type, b->ne[1]);
     const bool skinny = use_skinny(a->type, b->ne[1]);
-    const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
+    const int nc_max = nb ? (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb)) : 8;
     if (!mmq && !skinny && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
     if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
+    return TQ_STATUS_SUCCESS;
+}
+
+int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *workspace, size_t workspace_size,
+               void *stream) {
+    int rc;
+    if ((rc = check_mul_mat(a, b, dst))) return rc;
+    if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
+    const int nb = (int)(a->ne[0] / QK);
+    const bool pre_quantized = b->type == TQ_TYPE_Q8_K;
+    const bool mmq = use_mmq(a->type, b->ne[1]);
+    const bool skinny = use_skinny(a->type, b->ne[1]);
+    const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
 
     hipStream_t s = (hipStream_t)stream;
     void *q8 = b->data;
@@ -426,7 +444,7 @@ static int check_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_te
         (rc = check_tensor(dst, "dst")))
         return rc;
     if ((rc = check_weight_layout(as, "as")) || (rc = check_f32(b, "b")) || (rc = check_f32(dst, "dst"))) return rc;
-    if (ids->type != TQ_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4 || (uintptr_t)ids->data % 4)
+    if (ids->type != TQ_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4 || misaligned(ids->data, 4))
         return fail(TQ_STATUS_FAILED, "ids must be I32 with 4-byte elements");
     const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = b->ne[1];
     if (as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
@@ -620,6 +638,26 @@ int tq_moe_ffn(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down
     return TQ_STATUS_SUCCESS;
 }
 
+// The sum's dst [n_embd, T] with contiguous rows, and the slot rows as a contiguous [n_embd, n_used, T]
+// tensor at `slot_data` (in the workspace) checked as tq_moe_ffn's dst.
+static int check_moe_sum(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
+                         const tq_tensor *ids, const tq_tensor *weights, const tq_tensor *dst, void *slot_data,
+                         tq_tensor *so) {
+    int rc;
+    if (!gate || !up || !down || !b || !ids || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor");
+    if ((rc = check_tensor(dst, "dst")) || (rc = check_f32(dst, "dst"))) return rc;
+    if ((rc = check_tensor(gate, "gate")) || (rc = check_tensor(ids, "ids"))) return rc;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], n_embd = gate->ne[0];
+    if (dst->ne[0] != n_embd || dst->ne[1] != T || dst->ne[2] != 1 || dst->ne[3] != 1)
+        return fail(TQ_STATUS_FAILED, "dst shape is not [n_embd, T]");
+    if (dst->nb[0] != 4) return fail(TQ_STATUS_FAILED, "dst rows must be contiguous");
+    *so = tq_tensor{};
+    so->type = TQ_TYPE_F32, so->data = slot_data;
+    so->ne[0] = n_embd, so->ne[1] = n_used, so->ne[2] = T, so->ne[3] = 1;
+    so->nb[0] = 4, so->nb[1] = (size_t)n_embd * 4, so->nb[2] = so->nb[1] * n_used, so->nb[3] = so->nb[2] * T;
+    return check_moe(gate, up, down, b, ids, weights, so);
+}
+
 int tq_moe_ffn_sum(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *down, const tq_tensor *b,
                    const tq_tensor *ids, const tq_tensor *weights, tq_tensor *dst, void *workspace, size_t workspace_size,
                    void *stream) {
@@ -652,7 +690,7 @@ int tq_moe_ffn_sum(const tq_tensor *gate, const tq_tensor *up, const tq_tensor *
                      "sum_experts launch");
 }
 
-int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream) {
+static int check_sum_experts(const tq_tensor *experts, const tq_tensor *dst) {
     int rc;
     if (!experts || !dst) return fail(TQ_STATUS_FAILED, "NULL tensor");
     if ((rc = check_tensor(experts, "experts")) || (rc = check_f32(experts, "experts")) || (rc = check_tensor(dst, "dst")) ||
@@ -665,6 +703,13 @@ int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream) {
         return fail(TQ_STATUS_FAILED, "dst shape is not [n_embd, T]");
     if (experts->nb[0] != 4 || dst->nb[0] != 4) return fail(TQ_STATUS_FAILED, "rows must be contiguous");
     if (experts->nb[1] % 4 || experts->nb[2] % 4 || dst->nb[1] % 4) return fail(TQ_STATUS_FAILED, "unaligned strides");
+    return TQ_STATUS_SUCCESS;
+}
+
+int tq_sum_experts(const tq_tensor *experts, tq_tensor *dst, void *stream) {
+    int rc;
+    if ((rc = check_sum_experts(experts, dst))) return rc;
+    const int64_t n_embd = experts->ne[0], n_used = experts->ne[1], T = experts->ne[2];
     return check_hip(launch_sum_experts((const float *)experts->data, n_embd, (int)n_used, T, (int64_t)(experts->nb[1] / 4),
                                         (int64_t)(experts->nb[2] / 4), (float *)dst->data, (int64_t)(dst->nb[1] / 4),
                                         (hipStream_t)stream),
@@ -681,9 +726,8 @@ size_t tq_moe_router_workspace_size(const tq_tensor *gate_inp, const tq_tensor *
     return align_up((size_t)gate_inp->ne[1] * (size_t)ffn_inp->ne[1] * 4, 256);
 }
 
-int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_tensor *gate_inp, float eps, int n_used,
-                  tq_tensor *xn, tq_tensor *weights, tq_tensor *ids, void *workspace, size_t workspace_size,
-                  void *stream) {
+static int check_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_tensor *gate_inp, int n_used,
+                        const tq_tensor *xn, const tq_tensor *weights, const tq_tensor *ids) {
     int rc;
     if ((rc = check_tensor(ffn_inp, "ffn_inp")) || (rc = check_f32(ffn_inp, "ffn_inp")) ||
         (rc = check_tensor(ffn_norm, "ffn_norm")) || (rc = check_f32(ffn_norm, "ffn_norm")) ||
@@ -708,8 +752,17 @@ int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_
     if (weights->ne[0] != 1 || weights->ne[1] != n_used || weights->ne[2] != T || weights->ne[3] != 1)
         return fail(TQ_STATUS_FAILED, "weights shape is not [1, n_used, T]");
     if (ids->type != TQ_TYPE_I32 || ids->ne[0] != n_used || ids->ne[1] != T || ids->ne[2] != 1 || ids->ne[3] != 1 ||
-        ids->nb[0] % 4 || ids->nb[1] % 4 || (uintptr_t)ids->data % 4)
+        ids->nb[0] % 4 || ids->nb[1] % 4 || misaligned(ids->data, 4))
         return fail(TQ_STATUS_FAILED, "ids must be I32 [n_used, T]");
+    return TQ_STATUS_SUCCESS;
+}
+
+int tq_moe_router(const tq_tensor *ffn_inp, const tq_tensor *ffn_norm, const tq_tensor *gate_inp, float eps, int n_used,
+                  tq_tensor *xn, tq_tensor *weights, tq_tensor *ids, void *workspace, size_t workspace_size,
+                  void *stream) {
+    int rc;
+    if ((rc = check_router(ffn_inp, ffn_norm, gate_inp, n_used, xn, weights, ids))) return rc;
+    const int64_t n_embd = ffn_inp->ne[0], T = ffn_inp->ne[1], n_expert = gate_inp->ne[1];
     if (T == 0) return TQ_STATUS_SUCCESS;
     const size_t need = tq_moe_router_workspace_size(gate_inp, ffn_inp);
     if (workspace && workspace_size < need)
@@ -800,6 +853,33 @@ int tq_copy_expert_slots(const tq_tensor *src, const tq_tensor *dst, int n_tenso
         if ((rc = check_hip(launch_copy_slots(a, (hipStream_t)stream), "slot copy launch"))) return rc;
     }
     return TQ_STATUS_SUCCESS;
+}
+
+int tq_backend_supports_node(const tq_node *n) {
+    if (!n) return 0;
+    g_shape_only = true;
+    int rc;
+    switch (n->op) {
+    case TQ_NODE_MUL_MAT: rc = check_mul_mat(n->src[0], n->src[1], n->dst[0]); break;
+    case TQ_NODE_MUL_MAT_ID: rc = check_mul_mat_id(n->src[0], n->src[1], n->src[2], n->dst[0]); break;
+    case TQ_NODE_MOE_ROUTER:
+        rc = check_router(n->src[0], n->src[1], n->src[2], n->i_param, n->dst[0], n->dst[1], n->dst[2]);
+        break;
+    case TQ_NODE_MOE_FFN:
+        rc = !n->src[0] || !n->src[1] || !n->src[2] || !n->src[3] || !n->src[4] || !n->dst[0]
+                 ? fail(TQ_STATUS_FAILED, "NULL tensor")
+                 : check_moe(n->src[0], n->src[1], n->src[2], n->src[3], n->src[4], n->src[5], n->dst[0]);
+        break;
+    case TQ_NODE_MOE_FFN_SUM: {
+        tq_tensor so;
+        rc = check_moe_sum(n->src[0], n->src[1], n->src[2], n->src[3], n->src[4], n->src[5], n->dst[0], nullptr, &so);
+        break;
+    }
+    case TQ_NODE_SUM_EXPERTS: rc = check_sum_experts(n->src[0], n->dst[0]); break;
+    default: rc = fail(TQ_STATUS_FAILED, "node op %d is not one of this backend's", n->op);
+    }
+    g_shape_only = false;
+    return rc == TQ_STATUS_SUCCESS;
 }
 
 int tq_to_f32(int type, const void *src, float *dst, int64_t n, void *stream) {

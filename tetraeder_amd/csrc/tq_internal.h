@@ -9,6 +9,9 @@
 
 namespace tq {
 
+// Records the message of a failed call for tq_last_error() (this host thread) and returns code.
+int fail(int code, const char *fmt, ...);
+
 // Counters of the kernels whose workgroups count or wait for each other: the k split's tile arrivals,
 // the router's token arrivals and the MoE step's phase counts. Each stream that issues such a call gets
 // a block of its own from a file-scope device array (zero when the module loads; every call leaves the
