@@ -8,6 +8,7 @@ accumulation order differs). Then the Qwen3-30B-A3B expert shapes with top-8 rou
 expert-parallel rank share (other ranks' experts as -1), out-of-range ids and the golden fixtures.
 """
 import os
+import zlib
 import sys
 
 import numpy as np
@@ -175,3 +176,32 @@ def test_mul_mat_id_workspace_argument(gpu):
     assert torch.equal(c, d)
     with pytest.raises(ggml.Compute):
         ggml.mul_mat_id(w, b_big, ids_big, workspace=ws[: need // 2])
+
+
+@pytest.mark.parametrize("case", ["uniform_T128", "skew32_T128", "skew32_K4096_T128", "skew16_T128", "skew8_T256",
+                                  "neg90_T512", "q6_K_T128"])
+def test_mul_mat_id_prefill_routings(gpu, case):
+    """MUL_MAT_ID above 256 slots at the Qwen3-30B-A3B gate shape (Q4_K 2048 -> 768, 128 experts, top-8), on
+    the grouped MFMA kernel: uniform routing (about 8 tokens per expert, one 16-column chunk), every slot on
+    32 experts (32 tokens each: one 32-column chunk, activations staged in LDS; at K = 4096 the chunk does
+    not fit the LDS and the waves read the activations themselves), on 16 experts (64 tokens each: one
+    64-column chunk), on 8 experts (128 each: two chunks), 90% -1 (a few tokens on most experts); and a
+    Q6_K matrix (the GEMV path), all against the oracle."""
+    _case(case)
+    ty = ggml.Type.Q6_K if case.startswith("q6_K") else ggml.Type.Q4_K
+    k = 4096 if "_K4096" in case else 2048
+    n, E, used = 768, 128, 8
+    T = int(case.split("_T")[1])
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    ids = np.zeros((T, used), dtype=np.int32)
+    for t in range(T):
+        pool = {"skew32": 32, "skew16": 16, "skew8": 8}.get(case.split("_")[0], E)
+        ids[t] = rng.permutation(pool)[:used] if pool >= used else rng.integers(0, pool, used)
+    if case.startswith("neg90"):
+        ids[rng.random(ids.shape) < 0.9] = -1
+    w = make_experts(ty, k, n, E, seed=T + 5, device=gpu)
+    b = normal((T, 1, k), T + 6)
+    out = torch.full((T, used, n), 5.0, device=gpu)
+    ggml.mul_mat_id(w, torch.from_numpy(b).to(gpu), torch.from_numpy(ids).to(gpu), out=out)
+    want = O.mul_mat_id(ty.id, w.data.cpu().numpy(), k, n, E, b, ids)
+    check(out.cpu().numpy(), want, ids, case)

@@ -507,6 +507,8 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     m.d_s1 = (int64_t)(dst->nb[1] / 4);
     m.d_s2 = (int64_t)(dst->nb[2] / 4);
     m.route = ws ? (int32_t *)(ws + q8_bytes(b)) : nullptr;
+    m.chunk = mmid_mfma_chunk(as->type, m.n_expert, n_used * T);
+    m.q8_bytes = (int64_t)row_size(TQ_TYPE_Q8_K, b->ne[0]) * b->ne[1] * b->ne[2];
     if (n_used * T <= mmid_small_max_slots()) {
         // decode: one launch, routing resolved per workgroup, activations quantized in LDS
         const int b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0;
@@ -514,9 +516,15 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
                                                  (int64_t)(b->nb[2] / 4), b_vec, s),
                          "mul_mat_id launch");
     }
-    if ((rc = check_hip(launch_quantize_q8_K(b->data, b->ne[0], b->ne[1], b->ne[2], 1, b->nb[1], b->nb[2], b->nb[3], ws, s),
-                        "quantize_q8_K launch")))
-        return rc;
+    // the routing launch quantizes b as well (block indices are 32-bit: a Q8_K block stands for 1 KiB of
+    // F32 activations, so 2^31 of them would exceed the device memory)
+    const int64_t q8_blocks = b->ne[1] * b->ne[2] * (b->ne[0] / QK);
+    if (q8_blocks >= INT32_MAX) return fail(TQ_STATUS_FAILED, "%lld activation blocks", (long long)q8_blocks);
+    m.x = (const char *)b->data;
+    m.x_s1 = (int64_t)b->nb[1];
+    m.x_s2 = (int64_t)b->nb[2];
+    m.x_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0;
+    m.q8_blocks = (int32_t)q8_blocks;
     return check_hip(launch_mul_mat_id(as->type, m, s), "mul_mat_id launch");
 }
 

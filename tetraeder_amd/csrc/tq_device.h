@@ -147,6 +147,52 @@ template <int W> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// One Q8_K block quantized by a wave: lane l holds elements 4 l .. 4 l + 3 of the block in v and the
+// wave writes the 292 bytes at blkp. ggml's quantize_row_q8_K_ref (ggml-quants.c at b12426; called by
+// the reference at crates/ggml-sys/tests/iqk_kernels.rs:52,64):
+//   max = the first element with the largest |x| (a strict > scan), iscale = -127/max,
+//   qs = min(127, round-half-even(iscale*x)), bsums = sums of 16 qs, d = 1/iscale;
+//   an all-zero block gets d = 0 and qs = 0 (bsums are written as 0 here; ggml leaves them).
+// The division is IEEE correctly rounded (__fdiv_rn) and the product is not fused into anything, so
+// the bytes equal the CPU's. The parallel argmax keeps the first occurrence: among equal |x| the
+// smaller element index wins, which is what the left-to-right strict > scan selects (one 64-bit
+// maximum over the wave by DPP and permlane exchanges).
+__device__ __forceinline__ void quantize_q8k_wave(const float (&v)[4], uint8_t *blkp) {
+    const int lane = (int)(threadIdx.x & 63);
+    float amax = 0.f, vmax = 0.f;
+    int imax = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float a = fabsf(v[j]);
+        if (a > amax) amax = a, vmax = v[j], imax = lane * 4 + j;
+    }
+    // the wave's largest key: |x| bits (non-negative floats order as their bits) above the complemented
+    // index, so equal magnitudes go to the lower index
+    const uint64_t best = wave_max_u64(((uint64_t)__float_as_uint(amax) << 32) | (uint32_t)~imax);
+    amax = __uint_as_float(__builtin_amdgcn_readfirstlane((int)(uint32_t)(best >> 32)));
+    uint32_t packed = 0;
+    int s = 0;
+    float d = 0.f;
+    if (amax != 0.f) {
+        const int owner = __builtin_amdgcn_readfirstlane((int)(~(uint32_t)best) >> 2);
+        vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vmax), owner));
+        const float iscale = __fdiv_rn(-127.f, vmax);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int q = (int)rintf(__fmul_rn(iscale, v[j]));
+            q = q < 127 ? q : 127;
+            s += q;
+            packed |= (uint32_t)(q & 0xff) << (8 * j);
+        }
+        d = __fdiv_rn(1.f, iscale);
+    }
+    *(uint32_t *)(blkp + Q8K_QS + 4 * lane) = packed;
+    s += dpp_i<0xB1>(s);  // quad_perm [1,0,3,2]
+    s += dpp_i<0x4E>(s);  // quad_perm [2,3,0,1]
+    if ((lane & 3) == 0) *(int16_t *)(blkp + Q8K_BSUMS + 2 * (lane >> 2)) = (int16_t)s;
+    if (lane == 0) *(float *)blkp = d;
+}
+
 __device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 

@@ -117,9 +117,18 @@ struct MmidArgs {
     float *dst;              // [N, n_used, T]
     int64_t d_s1, d_s2;      // floats
     int32_t *route;          // workspace: routing lists (mmid_route_bytes)
+    int32_t chunk;           // grouped MFMA kernel: columns per work item (0: the GEMV kernel, no items)
+    int64_t q8_bytes;        // bytes of the Q8_K rows at q8
+    // the F32 activations [K, ne11, T] the routing launch quantizes into q8 (q8_blocks Q8_K blocks)
+    const char *x;
+    int64_t x_s1, x_s2;      // bytes
+    int32_t x_vec;           // x and its strides are 16-byte aligned
+    int32_t q8_blocks;
 };
 size_t mmid_route_bytes(int n_expert, int64_t n_slots);
 hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream);
+// Columns per work item of the grouped int8-MFMA MUL_MAT_ID for these operands (0: the GEMV kernel)
+int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots);
 // decode-size routing (n_used * T <= 256): one launch, F32 activations quantized in each workgroup
 constexpr int64_t mmid_small_max_slots() { return 256; }
 hipError_t launch_mul_mat_id_small(int type, const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,

@@ -5,15 +5,21 @@
 // 214-253) an id < 0 reads no weights and its dst row is exactly zero.
 //
 // Two launches, no host synchronization (the ids never leave the device):
-//   k_mmid_route  workgroup 0 compacts the routing: per-expert slot counts (LDS atomics), a scan into
-//                 per-expert column ranges, the list of routed experts and each expert's slots;
-//                 workgroups 1.. write the zero rows of slots whose id is negative (or >= n_expert);
+//   k_mmid_prep   workgroup 0 compacts the routing: per-expert slot counts (LDS atomics), a scan into
+//                 per-expert column ranges, the list of routed experts, each expert's slots and the
+//                 work items of the grouped MFMA kernel; the next workgroups quantize the activation
+//                 rows to Q8_K (one wave per block) and the last ones write the zero rows of slots whose
+//                 id is negative (or >= n_expert), all at once;
 //   k_mmid_gemv   grid.y walks the routed experts (workgroups past the routed count exit at once),
 //                 grid.x splits an expert's rows; each workgroup stages its expert's columns (the
 //                 tokens routed to it, up to 8 at a time) in LDS and streams the expert's weights once
-//                 for all of them with the GEMV core.
+//                 for all of them with the GEMV core;
+//   or, Q4_K experts with several tokens each (prefill), k_mmid_mfma_q4k: grid.y walks the work items
+//                 (a chunk of up to 16 MT columns of one routed expert), grid.x the expert's 128-row
+//                 tiles; a workgroup runs the skinny int8-MFMA step of tq_skinny.h over its chunk.
 #include "tq_gemv_core.h"
 #include "tq_internal.h"
+#include "tq_skinny.h"
 
 #include <algorithm>
 #include <cmath>
@@ -21,64 +27,90 @@
 
 namespace tq {
 
-constexpr int ROUTE_THREADS = 256;
+constexpr int PREP_THREADS = 512;
+constexpr int PREP_WAVES = PREP_THREADS / 64;
 constexpr int MMID_NC = 8;  // columns staged per pass
+// slots per routed expert (uniform routing) from which Q4_K experts run on the grouped MFMA kernel
+#ifndef TQ_MMID_MFMA_MIN_COLS
+#define TQ_MMID_MFMA_MIN_COLS 4
+#endif
+constexpr double MMID_MFMA_MIN_COLS = TQ_MMID_MFMA_MIN_COLS;
 
-// Workspace layout (int32): [0] routed expert count, [1] valid slot count, then
-// expert[n_expert], start[n_expert], count[n_expert], slot[n_slots].
-size_t mmid_route_bytes(int n_expert, int64_t n_slots) { return 4 * (2 + 3 * (size_t)n_expert + (size_t)n_slots); }
+// Workspace layout (int32): [0] routed expert count, [1] valid slot count, [2] work items, [3] unused,
+// then expert[n_expert], start[n_expert], count[n_expert], slot[n_slots] (the GEMV kernel's lists), and
+// from a multiple of four ints the grouped MFMA kernel's work items: chunks of up to `chunk` columns of a
+// routed expert, each a record of 4 + chunk ints {expert, columns, 0, 0, slot of each column}
+// (max_items = min(n_expert, n_slots) + ceil(n_slots / chunk)).
+constexpr int MMID_HDR = 4;
+constexpr int MMID_CHUNKS[3] = {16, 32, 64};
+__host__ __device__ static int64_t mmid_max_items(int n_expert, int64_t n_slots, int chunk) {
+    return (n_expert < n_slots ? n_expert : n_slots) + (n_slots + chunk - 1) / chunk;
+}
+__host__ __device__ static int64_t mmid_items_offset(int n_expert, int64_t n_slots) {
+    return (MMID_HDR + 3 * (int64_t)n_expert + n_slots + 3) & ~(int64_t)3;
+}
+size_t mmid_route_bytes(int n_expert, int64_t n_slots) {
+    int64_t items = 0;
+    for (int ch : MMID_CHUNKS) items = std::max<int64_t>(items, mmid_max_items(n_expert, n_slots, ch) * (4 + ch));
+    return 4 * (size_t)(mmid_items_offset(n_expert, n_slots) + items);
+}
 
 __device__ __forceinline__ int load_id(const uint8_t *ids, int64_t s0, int64_t s1, int n_used, int s) {
     const int j = s % n_used, t = s / n_used;
     return *(const int32_t *)(ids + j * s0 + t * s1);
 }
 
-// Exclusive scan of v over the 256 threads of the block; returns the prefix, *total gets the sum.
-__device__ int block_exclusive_scan(int v, int *lds_tmp, int *total) {
+// Exclusive scans of the three values v[] over the PREP_THREADS threads of the block, in place; total[]
+// gets their sums (lds_tmp: 3 PREP_WAVES ints).
+__device__ void block_exclusive_scan3(int (&v)[3], int *lds_tmp, int (&total)[3]) {
     const int lane = lane_id(), wid = threadIdx.x >> 6;
-    const int x = wave_incl_scan(v);
-    if (lane == 63) lds_tmp[wid] = x;
-    __syncthreads();
-    int base = 0, sum = 0;
-    for (int w = 0; w < ROUTE_THREADS / 64; ++w) {
-        if (w < wid) base += lds_tmp[w];
-        sum += lds_tmp[w];
+    int x[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        x[k] = wave_incl_scan(v[k]);
+        if (lane == 63) lds_tmp[3 * wid + k] = x[k];
     }
     __syncthreads();
-    *total = sum;
-    return base + x - v;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        int base = 0, sum = 0;
+        for (int w = 0; w < PREP_WAVES; ++w) {
+            if (w < wid) base += lds_tmp[3 * w + k];
+            sum += lds_tmp[3 * w + k];
+        }
+        total[k] = sum;
+        v[k] = base + x[k] - v[k];
+    }
 }
 
-constexpr int ROUTE_IDS = 8;  // ids per thread in flight while routing
+constexpr int ROUTE_IDS = 16;   // ids a routing thread reads at once and keeps (PREP_THREADS x 16 slots)
+constexpr int ZERO_SLOTS = 64;  // slots whose zero rows one workgroup writes
 
-__global__ __launch_bounds__(ROUTE_THREADS) void k_mmid_route(MmidArgs a) {
+// The routing lists (workgroup 0 of k_mmid_prep).
+__device__ void mmid_route(const MmidArgs &a, int *lds_i) {
     const int n_slots = a.n_used * a.ntok, E = a.n_expert;
-    if (blockIdx.x > 0) {
-        // zero rows: slots with an id outside [0, n_expert) read nothing and give exact zeros
-        for (int s = blockIdx.x - 1; s < n_slots; s += gridDim.x - 1) {
-            const int e = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, s);
-            if (e >= 0 && e < E) continue;
-            const int j = s % a.n_used, t = s / a.n_used;
-            float *row = a.dst + j * a.d_s1 + t * a.d_s2;
-            for (int i = threadIdx.x; i < a.nrows; i += ROUTE_THREADS) row[i] = 0.f;
-        }
-        return;
-    }
-    extern __shared__ int lds_i[];
-    int *cnt = lds_i, *pos = lds_i + E, *tmp = lds_i + 2 * E;
-    for (int e = threadIdx.x; e < E; e += ROUTE_THREADS) cnt[e] = 0;
+    int *cnt = lds_i, *pos = lds_i + E, *ibase = lds_i + 2 * E, *tmp = lds_i + 3 * E;
+    for (int e = threadIdx.x; e < E; e += PREP_THREADS) cnt[e] = 0;
     __syncthreads();
     // ids are read ROUTE_IDS per thread at a time, all in flight together (clamped index, masked use):
     // a loop of one load and one atomic per slot would wait for every load
     auto ids_batch = [&](int s0, int (&ev)[ROUTE_IDS]) {
 #pragma unroll
         for (int i = 0; i < ROUTE_IDS; ++i)
-            ev[i] = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, min(s0 + i * ROUTE_THREADS, n_slots - 1));
+            ev[i] = load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, min(s0 + i * PREP_THREADS, n_slots - 1));
 #pragma unroll
         for (int i = 0; i < ROUTE_IDS; ++i)
-            if (s0 + i * ROUTE_THREADS >= n_slots || ev[i] < 0 || ev[i] >= E) ev[i] = -1;
+            if (s0 + i * PREP_THREADS >= n_slots || ev[i] < 0 || ev[i] >= E) ev[i] = -1;
     };
-    for (int s0 = threadIdx.x; s0 < n_slots; s0 += ROUTE_IDS * ROUTE_THREADS) {
+    // the first batch stays in registers for the scatter; later batches (above PREP_THREADS x ROUTE_IDS
+    // slots) are read again
+    constexpr int BATCH = ROUTE_IDS * PREP_THREADS;
+    int ev0[ROUTE_IDS];
+    ids_batch(threadIdx.x, ev0);
+#pragma unroll
+    for (int i = 0; i < ROUTE_IDS; ++i)
+        if (ev0[i] >= 0) atomicAdd(&cnt[ev0[i]], 1);
+    for (int s0 = threadIdx.x + BATCH; s0 < n_slots; s0 += BATCH) {
         int ev[ROUTE_IDS];
         ids_batch(s0, ev);
 #pragma unroll
@@ -87,30 +119,89 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_mmid_route(MmidArgs a) {
     }
     __syncthreads();
     // each thread scans a contiguous chunk of experts
-    const int chunk = (E + ROUTE_THREADS - 1) / ROUTE_THREADS;
+    const int chunk = (E + PREP_THREADS - 1) / PREP_THREADS;
     const int e0 = min(E, (int)threadIdx.x * chunk), e1 = min(E, e0 + chunk);
     int my_cnt = 0, my_act = 0;
     for (int e = e0; e < e1; ++e) my_cnt += cnt[e], my_act += cnt[e] > 0;
-    int n_valid, n_active;
-    int start = block_exclusive_scan(my_cnt, tmp, &n_valid);
-    int act = block_exclusive_scan(my_act, tmp, &n_active);
-    int32_t *expert = a.route + 2, *ex_start = expert + E, *ex_count = ex_start + E, *slot = ex_count + E;
+    // work items of the grouped MFMA kernel: one per `chunk` columns of each routed expert
+    const int ch = a.chunk > 0 ? a.chunk : 1, ch_log2 = 31 - __builtin_clz(ch);
+    int my_items = 0;
+    if (a.chunk > 0)
+        for (int e = e0; e < e1; ++e) my_items += (cnt[e] + ch - 1) >> ch_log2;
+    int v[3] = {my_cnt, my_act, my_items}, tot[3];
+    block_exclusive_scan3(v, tmp, tot);
+    int start = v[0], act = v[1], item = v[2];
+    int32_t *expert = a.route + MMID_HDR, *ex_start = expert + E, *ex_count = ex_start + E, *slot = ex_count + E;
+    int32_t *items = a.route + mmid_items_offset(E, n_slots);
+    const int rec = 4 + ch;  // ints per work item record
     for (int e = e0; e < e1; ++e) {
-        pos[e] = start;
+        // the scatter ranks an expert's slots from its start (slot[]) or from 0 (item records)
+        pos[e] = a.chunk > 0 ? 0 : start;
+        ibase[e] = item;
         if (cnt[e] > 0) {
             expert[act] = e, ex_start[act] = start, ex_count[act] = cnt[e];
+            if (a.chunk > 0)
+                for (int c0 = 0; c0 < cnt[e]; c0 += ch, ++item)
+                    *(int4 *)(items + (int64_t)item * rec) = int4{e, min(ch, cnt[e] - c0), 0, 0};
             ++act;
         }
         start += cnt[e];
     }
-    if (threadIdx.x == 0) a.route[0] = n_active, a.route[1] = n_valid;
+    if (threadIdx.x == 0) a.route[0] = tot[1], a.route[1] = tot[0], a.route[2] = a.chunk > 0 ? tot[2] : 0;
     __syncthreads();
-    for (int s0 = threadIdx.x; s0 < n_slots; s0 += ROUTE_IDS * ROUTE_THREADS) {
+    auto place = [&](int e, int s) {
+        const int p = atomicAdd(&pos[e], 1);
+        if (a.chunk > 0) items[(int64_t)(ibase[e] + (p >> ch_log2)) * rec + 4 + (p & (ch - 1))] = s;
+        else slot[p] = s;
+    };
+#pragma unroll
+    for (int i = 0; i < ROUTE_IDS; ++i)
+        if (ev0[i] >= 0) place(ev0[i], threadIdx.x + i * PREP_THREADS);
+    for (int s0 = threadIdx.x + BATCH; s0 < n_slots; s0 += BATCH) {
         int ev[ROUTE_IDS];
         ids_batch(s0, ev);
 #pragma unroll
         for (int i = 0; i < ROUTE_IDS; ++i)
-            if (ev[i] >= 0) slot[atomicAdd(&pos[ev[i]], 1)] = s0 + i * ROUTE_THREADS;
+            if (ev[i] >= 0) place(ev[i], s0 + i * PREP_THREADS);
+    }
+}
+
+// Workgroup 0 routes; workgroups 1 .. q8_wgs quantize the activation rows (a wave per Q8_K block, rows
+// t * ne11 + i1 of ne11 per token); the rest write the zero rows of ZERO_SLOTS slots each.
+__global__ __launch_bounds__(PREP_THREADS) void k_mmid_prep(MmidArgs a, int q8_wgs) {
+    extern __shared__ int lds_i[];
+    if (blockIdx.x == 0) {
+        mmid_route(a, lds_i);
+        return;
+    }
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    if ((int)blockIdx.x <= q8_wgs) {
+        const int g = (blockIdx.x - 1) * PREP_WAVES + wave;
+        if (g >= a.q8_blocks) return;
+        const int r = g / a.nb, blk = g - r * a.nb, i1 = r % a.ne11, t = r / a.ne11;
+        const float *src = (const float *)(a.x + i1 * a.x_s1 + t * a.x_s2) + blk * QK + lane * 4;
+        float v[4];
+        if (a.x_vec) {
+            const float4 f = *(const float4 *)src;
+            v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = src[j];
+        }
+        quantize_q8k_wave(v, (uint8_t *)a.q8 + (size_t)g * Q8K_BYTES);
+        return;
+    }
+    // zero rows: slots with an id outside [0, n_expert) read nothing and give exact zeros; the k-th such
+    // slot of the workgroup's ZERO_SLOTS goes to wave k % PREP_WAVES
+    const int n_slots = a.n_used * a.ntok, s0 = (blockIdx.x - 1 - q8_wgs) * ZERO_SLOTS;
+    const int s = s0 + lane;
+    const int e = s < n_slots ? load_id(a.ids, a.ids_s0, a.ids_s1, a.n_used, s) : 0;
+    uint64_t neg = __ballot(s < n_slots && (e < 0 || e >= a.n_expert));
+    for (int k = 0; neg; ++k, neg &= neg - 1) {
+        if (k % PREP_WAVES != wave) continue;
+        const int sl = s0 + __builtin_ctzll(neg), j = sl % a.n_used, t = sl / a.n_used;
+        float *row = a.dst + j * a.d_s1 + t * a.d_s2;
+        for (int i = lane; i < a.nrows; i += 64) row[i] = 0.f;
     }
 }
 
@@ -148,7 +239,7 @@ template <int F, int LPR>
 __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_gemv(MmidArgs a) {
     const int ai = blockIdx.y;
     if (ai >= a.route[0]) return;  // fewer experts routed than grid rows: the whole workgroup leaves
-    const int32_t *expert = a.route + 2, *ex_start = expert + a.n_expert, *ex_count = ex_start + a.n_expert;
+    const int32_t *expert = a.route + MMID_HDR, *ex_start = expert + a.n_expert, *ex_count = ex_start + a.n_expert;
     const int32_t *slot = ex_count + a.n_expert;
     const int e = expert[ai], start = ex_start[ai], cnt = ex_count[ai];
     const uint8_t *w = a.w + (int64_t)e * a.w_s2;
@@ -167,6 +258,130 @@ __global__ __launch_bounds__(GEMV_WAVES * 64) void k_mmid_gemv(MmidArgs a) {
         else if (n <= 4) mmid_pass<F, 4, LPR>(a, w, slots, n, lds_qs, lds_bs, lds_d, col_dst);
         else mmid_pass<F, 8, LPR>(a, w, slots, n, lds_qs, lds_bs, lds_d, col_dst);
     }
+}
+
+// Grouped int8-MFMA MUL_MAT_ID over Q4_K experts (the work items of k_mmid_prep): workgroup (x, y) owns
+// rows 128 x .. 128 x + 127 of the expert of work item y, one 16-row tile per wave, and the item's
+// columns (up to 16 MT). A wave walks all super-blocks of its tile with the weights of the next ones in
+// flight while it computes the current one, and stores its own rows (no reduction across waves).
+constexpr int MMID_SK_WAVES = 8;
+constexpr int MMID_SK_ROWS = 16 * MMID_SK_WAVES;  // rows per workgroup
+constexpr size_t MMID_ACT_LDS_MAX = 150 * 1024;    // dynamic LDS for a staged activation chunk
+
+// LDS bytes of a chunk of ncol staged activation columns over nb super-blocks (qs, S_j, d).
+static size_t mmid_act_lds(int nb, int ncol) { return (size_t)nb * ncol * (256 + 4 * 8 + 4); }
+
+// LDS_ACT: the chunk's activation blocks are staged in LDS once per workgroup (the qs by wave-wide LDS
+// DMAs of four blocks each, the bsums and d by the lanes) and every wave reads its operands there;
+// without it every wave loads them from the cache hierarchy itself (eight times the traffic).
+template <int MT, bool LDS_ACT>
+__device__ __forceinline__ void mmid_mfma_q4k(const MmidArgs &a, uint8_t *lds_act) {
+    __shared__ int64_t col_q8[16 * MT], col_dst[16 * MT];  // a column's Q8_K row (bytes) and dst row (floats)
+    constexpr int NCOL = 16 * MT;
+    const int item = blockIdx.y;
+    const int n_slots = a.n_used * a.ntok;
+    // the item count and the item's record (header and column slots) are read at once (a record exists
+    // for every grid row; its slots past the column count are not used)
+    const int n_items = a.route[2];
+    const int32_t *rec = a.route + mmid_items_offset(a.n_expert, n_slots) + (int64_t)item * (4 + NCOL);
+    const int4 hdr = *(const int4 *)rec;
+    const int my_slot = (int)threadIdx.x < NCOL ? rec[4 + threadIdx.x] : 0;
+    if (item >= n_items) return;  // fewer work items than grid rows: the whole workgroup leaves
+    const int e = hdr.x, nvalid = hdr.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int nb = a.nb;
+    const int64_t row = (int64_t)blockIdx.x * MMID_SK_ROWS + 16 * wave + n;
+    const bool rv = row < a.nrows;
+    const uint8_t *wrow = a.w + (int64_t)e * a.w_s2 + (rv ? row : 0) * a.w_s1;
+    // the first super-blocks' weights are in flight while the columns are resolved and staged; PF
+    // register sets rotate (as many as the operand registers of MT tiles leave room for)
+    constexpr int PF = MT == 1 ? 3 : 2;
+    Q4kLaneBlock wr[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) wr[i].load(wrow + (int64_t)min(i, nb - 1) * Q4K_BYTES);
+    if ((int)threadIdx.x < nvalid) {
+        const int s = my_slot, j = s % a.n_used, t = s / a.n_used;
+        col_q8[threadIdx.x] = ((int64_t)t * a.ne11 + j % a.ne11) * nb * Q8K_BYTES;
+        col_dst[threadIdx.x] = j * a.d_s1 + t * a.d_s2;
+    }
+    lds_barrier();  // the weight loads stay in flight
+    v4f acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct) acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int ntile = (nvalid + 15) >> 4;  // tiles with a valid column (the rest are skipped)
+    uint8_t *s_qs = lds_act;
+    float *s_S = (float *)(lds_act + (size_t)nb * NCOL * 256), *s_D = s_S + (size_t)nb * NCOL * 8;
+    if constexpr (LDS_ACT) {
+        // qs: four (b, k) pairs per wave-wide DMA of 16 bytes a lane, lane l writing piece l % 16 of pair
+        // 4 q + l / 16 and reading the piece that belongs there (the Q8_K rows are the buffer resource,
+        // so every offset stays inside them; columns past nvalid repeat the last column)
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.q8, (short)0, (int)a.q8_bytes, BUFFER_FLAGS);
+        const int kgroups = (nvalid + 3) >> 2;
+        for (int q = wave; q < nb * kgroups; q += MMID_SK_WAVES) {
+            const int b = q / kgroups, k0 = 4 * (q - b * kgroups), k = k0 + (lane >> 4);
+            const uint32_t off = (uint32_t)(col_q8[min(k, nvalid - 1)] + (int64_t)b * Q8K_BYTES) + Q8K_QS +
+                                 16 * ((lane & 15) ^ (k & 15));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void *)(s_qs + 256 * (b * NCOL + k0)), 16, off, 0, 0, 0);
+        }
+        // the 32-sums S_j (word j of the bsums: two 16-sums) and d of each (b, k), as floats
+        for (int i = threadIdx.x; i < nb * nvalid * 9; i += MMID_SK_WAVES * 64) {
+            const int p = i / 9, wd = i - p * 9;
+            const int b = p / nvalid, k = p - b * nvalid;
+            const uint8_t *blk = a.q8 + col_q8[k] + (int64_t)b * Q8K_BYTES;
+            if (wd < 8) s_S[8 * (b * NCOL + k) + wd] = bsums_pair(*(const uint32_t *)(blk + Q8K_BSUMS + 4 * wd));
+            else s_D[b * NCOL + k] = *(const float *)blk;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+    // super-block b from register set b % PF, which then loads block b + PF (clamped: the last blocks
+    // load the final one again, from the cache)
+    auto step = [&](Q4kLaneBlock &w, int b) {
+        Q4kPlanes P;
+        q4k_planes(w, rv, P);
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct) {
+            if (ct < ntile) {
+                Q4kTileAct t;
+                if constexpr (LDS_ACT) {
+                    load_tile_act_lds(t, s_qs, s_S, s_D, b * NCOL + 16 * ct);
+                } else {
+                    load_tile_act(t, 16 * ct, nvalid, [&](int k) { return a.q8 + col_q8[k] + (int64_t)b * Q8K_BYTES; });
+                }
+                q4k_tile_mma(P, t, acc[ct]);
+            }
+        }
+        w.load(wrow + (int64_t)min(b + PF, nb - 1) * Q4K_BYTES);
+    };
+    for (int b = 0; b < nb; b += PF) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i)
+            if (b + i < nb) step(wr[i], b + i);
+    }
+    if (rv) {
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = 16 * ct + 4 * g + i;
+                if (k < nvalid) a.dst[col_dst[k] + row] = acc[ct][i];
+            }
+    }
+}
+
+template <int MT>
+__global__ __launch_bounds__(MMID_SK_WAVES * 64) __attribute__((amdgpu_waves_per_eu(MT <= 2 ? 4 : 2)))
+void k_mmid_mfma_q4k_lds(MmidArgs a) {
+    extern __shared__ __align__(16) uint8_t lds_act[];
+    mmid_mfma_q4k<MT, true>(a, lds_act);
+}
+
+template <int MT>
+__global__ __launch_bounds__(MMID_SK_WAVES * 64) __attribute__((amdgpu_waves_per_eu(MT <= 2 ? 4 : 2)))
+void k_mmid_mfma_q4k(MmidArgs a) {
+    mmid_mfma_q4k<MT, false>(a, nullptr);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -479,13 +694,42 @@ static hipError_t launch_fmt(const MmidArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots) {
+    if (type != FMT_Q4K || n_slots <= 0) return 0;
+    const double per_expert = (double)n_slots / (double)std::min<int64_t>(n_expert, n_slots);
+    if (per_expert < MMID_MFMA_MIN_COLS) return 0;
+    return per_expert <= 16 ? 16 : per_expert <= 32 ? 32 : 64;
+}
+
 hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream) {
     const int64_t n_slots = (int64_t)a.n_used * a.ntok;
     if (n_slots == 0) return hipSuccess;
-    const unsigned zero_blocks = (unsigned)std::min<int64_t>(n_slots, 256);
-    k_mmid_route<<<1 + zero_blocks, ROUTE_THREADS, (2 * a.n_expert + ROUTE_THREADS / 64) * sizeof(int), stream>>>(a);
+    const int q8_wgs = (int)((a.q8_blocks + PREP_WAVES - 1) / PREP_WAVES);
+    const int zero_wgs = (int)((n_slots + ZERO_SLOTS - 1) / ZERO_SLOTS);
+    k_mmid_prep<<<1 + q8_wgs + zero_wgs, PREP_THREADS, (3 * a.n_expert + 3 * PREP_WAVES) * sizeof(int), stream>>>(a, q8_wgs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // Q4_K experts with several tokens each on average: the grouped int8-MFMA kernel over the work items
+    // (chunks of a routed expert's columns) the routing pass listed
+    if (a.chunk > 0) {
+        const dim3 grid((unsigned)((a.nrows + MMID_SK_ROWS - 1) / MMID_SK_ROWS),
+                        (unsigned)mmid_max_items(a.n_expert, n_slots, a.chunk));
+        const int mt = a.chunk / 16;
+        // the staged activation chunk must fit the LDS next to the kernel's own arrays (and its offsets
+        // the 32-bit range of a buffer resource)
+        const size_t lds = mmid_act_lds(a.nb, a.chunk);
+        const bool lds_act = lds <= MMID_ACT_LDS_MAX && a.q8_bytes < (1ll << 31);
+        if (lds_act) {
+            if (mt == 1) k_mmid_mfma_q4k_lds<1><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            else if (mt == 2) k_mmid_mfma_q4k_lds<2><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            else k_mmid_mfma_q4k_lds<4><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+        } else {
+            if (mt == 1) k_mmid_mfma_q4k<1><<<grid, MMID_SK_WAVES * 64, 0, stream>>>(a);
+            else if (mt == 2) k_mmid_mfma_q4k<2><<<grid, MMID_SK_WAVES * 64, 0, stream>>>(a);
+            else k_mmid_mfma_q4k<4><<<grid, MMID_SK_WAVES * 64, 0, stream>>>(a);
+        }
+        return hipGetLastError();
+    }
     return type == FMT_Q4K ? launch_fmt<FMT_Q4K>(a, stream) : launch_fmt<FMT_Q6K>(a, stream);
 }
 

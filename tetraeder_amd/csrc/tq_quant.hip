@@ -6,16 +6,8 @@
 namespace tq {
 
 // ---------------------------------------------------------------------------------------------
-// Q8_K: one wave64 per 256-element block, four consecutive floats per lane (one 16-byte load).
-// ggml's quantize_row_q8_K_ref (ggml-quants.c at b12426; called by the reference at
-// crates/ggml-sys/tests/iqk_kernels.rs:52,64):
-//   max = the first element with the largest |x| (a strict > scan), iscale = -127/max,
-//   qs = min(127, round-half-even(iscale*x)), bsums = sums of 16 qs, d = 1/iscale;
-//   an all-zero block gets d = 0 and qs = 0 (bsums are written as 0 here; ggml leaves them).
-// The division is IEEE correctly rounded (__fdiv_rn) and the product is not fused into anything, so
-// the bytes equal the CPU's. The parallel argmax keeps the first occurrence: among equal |x| the
-// smaller element index wins, which is what the left-to-right strict > scan selects (one 64-bit
-// maximum over the wave by DPP and permlane exchanges).
+// Q8_K: one wave64 per 256-element block, four consecutive floats per lane (one 16-byte load), the
+// block quantized by quantize_q8k_wave (bit-exact with ggml's quantize_row_q8_K_ref).
 // ---------------------------------------------------------------------------------------------
 // I: the index type of the block arithmetic (32-bit divisions are a few instructions, 64-bit ones a
 // subroutine each).
@@ -36,39 +28,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const char *__restrict__ 
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[j];
     }
-    float amax = 0.f, vmax = 0.f;
-    int imax = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float a = fabsf(v[j]);
-        if (a > amax) amax = a, vmax = v[j], imax = lane * 4 + j;
-    }
-    // the wave's largest key: |x| bits (non-negative floats order as their bits) above the complemented
-    // index, so equal magnitudes go to the lower index
-    const uint64_t best = wave_max_u64(((uint64_t)__float_as_uint(amax) << 32) | (uint32_t)~imax);
-    amax = __uint_as_float(__builtin_amdgcn_readfirstlane((int)(uint32_t)(best >> 32)));
-    uint8_t *blkp = y + (size_t)g * Q8K_BYTES;
-    uint32_t packed = 0;
-    int s = 0;
-    float d = 0.f;
-    if (amax != 0.f) {
-        const int owner = __builtin_amdgcn_readfirstlane((int)(~(uint32_t)best) >> 2);
-        vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vmax), owner));
-        const float iscale = __fdiv_rn(-127.f, vmax);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int q = (int)rintf(__fmul_rn(iscale, v[j]));
-            q = q < 127 ? q : 127;
-            s += q;
-            packed |= (uint32_t)(q & 0xff) << (8 * j);
-        }
-        d = __fdiv_rn(1.f, iscale);
-    }
-    *(uint32_t *)(blkp + Q8K_QS + 4 * lane) = packed;
-    s += dpp_i<0xB1>(s);  // quad_perm [1,0,3,2]
-    s += dpp_i<0x4E>(s);  // quad_perm [2,3,0,1]
-    if ((lane & 3) == 0) *(int16_t *)(blkp + Q8K_BSUMS + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *(float *)blkp = d;
+    quantize_q8k_wave(v, y + (size_t)g * Q8K_BYTES);
 }
 
 hipError_t launch_quantize_q8_K(const void *x, int64_t k, int64_t ne1, int64_t ne2, int64_t ne3, size_t s1, size_t s2,
