@@ -384,6 +384,121 @@ void k_mmid_mfma_q4k(MmidArgs a) {
     mmid_mfma_q4k<MT, false>(a, nullptr);
 }
 
+// The same work split over K instead of rows, for K = 2048 (8 super-blocks, one per wave): wave w owns
+// super-block w of all 8 row tiles of the workgroup and keeps the chunk's activation operands for it in
+// registers. The row tiles (16 rows x 1152 bytes, contiguous in the expert) come into LDS by wave-wide
+// LDS DMAs of 64 x 16 bytes, two tiles ahead in three buffers; the 8 waves' partial sums of a tile meet
+// in LDS, where all lanes add them up and store the tile. Every DMA reads one kilobyte of consecutive
+// weight bytes: HBM serves that far better than the MFMA operand layout read straight from memory (16
+// rows' pieces a row length apart in every load).
+constexpr int KS_NB = 8;                                   // super-blocks per row
+constexpr int KS_PIECES = 16 * KS_NB * Q4K_BYTES / 16;     // 16-byte pieces of a row tile (1152)
+constexpr int KS_ROW_PIECES = KS_NB * Q4K_BYTES / 16;      // per row (72)
+constexpr int KS_DMAS = KS_PIECES / 64;                    // wave-wide DMAs per tile (18)
+static_assert(KS_PIECES % 64 == 0, "whole DMAs per tile");
+
+// LDS position (16-byte units) of piece c of row n in a staged tile: rows rotated by n pieces, so the
+// same piece of 16 rows lands in 16 different groups of 4 banks.
+__device__ __forceinline__ int ks_pos(int n, int c) {
+    const int r = c + n;
+    return KS_ROW_PIECES * n + (r >= KS_ROW_PIECES ? r - KS_ROW_PIECES : r);
+}
+
+template <int MT>
+__global__ __launch_bounds__(MMID_SK_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void k_mmid_ksplit_q4k(MmidArgs a) {
+    static_assert(MMID_SK_WAVES == KS_NB, "one super-block per wave");
+    constexpr int NCOL = 16 * MT, W = MMID_SK_WAVES, RT = MMID_SK_ROWS / 16, NBUF = 3;
+    __shared__ __align__(16) uint8_t tiles[NBUF][KS_PIECES * 16];
+    __shared__ v4f red[W][MT][64];  // the waves' partial sums of a tile
+    __shared__ int64_t col_q8[NCOL], col_dst[NCOL];
+    const int item = blockIdx.y;
+    const int n_slots = a.n_used * a.ntok;
+    const int n_items = a.route[2];
+    const int32_t *rec = a.route + mmid_items_offset(a.n_expert, n_slots) + (int64_t)item * (4 + NCOL);
+    const int4 hdr = *(const int4 *)rec;
+    const int my_slot = (int)threadIdx.x < NCOL ? rec[4 + threadIdx.x] : 0;
+    if (item >= n_items) return;  // fewer work items than grid rows: the whole workgroup leaves
+    const int e = hdr.x, nvalid = hdr.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int64_t r0 = (int64_t)blockIdx.x * MMID_SK_ROWS;
+    const int nt = (int)min<int64_t>(RT, (a.nrows - r0 + 15) / 16);  // row tiles with a row in range
+    const uint8_t *wexp = a.w + (int64_t)e * a.w_s2;
+    if ((int)threadIdx.x < nvalid) {
+        const int s = my_slot, j = s % a.n_used, t = s / a.n_used;
+        col_q8[threadIdx.x] = ((int64_t)t * a.ne11 + j % a.ne11) * KS_NB * Q8K_BYTES;
+        col_dst[threadIdx.x] = j * a.d_s1 + t * a.d_s2;
+    }
+    lds_barrier();
+    const int ntile = (nvalid + 15) >> 4;  // column tiles with a valid column (the rest are skipped)
+    Q4kTileAct act[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct)
+        if (ct < ntile)
+            load_tile_act(act[ct], 16 * ct, nvalid, [&](int k) { return a.q8 + col_q8[k] + (int64_t)wave * Q8K_BYTES; });
+    // DMA q of a tile (q = wave, wave + 8, ...): lane l fetches the piece that belongs at LDS position
+    // 64 q + l; the tile's rows are the buffer resource (rows past the end read as zeros)
+    const int ndma = (KS_DMAS - wave + W - 1) / W;  // this wave's DMAs per tile (3 or 2)
+    auto dma_tile = [&](int t) {
+        const int64_t rt = r0 + 16 * t;
+        const int64_t rows = min<int64_t>(16, a.nrows - rt);
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(wexp + rt * a.w_s1), (short)0, (int)(rows * a.w_s1), BUFFER_FLAGS);
+        uint8_t *buf = tiles[t % NBUF];
+        for (int q = wave; q < KS_DMAS; q += W) {
+            const int p = 64 * q + lane, rn = p / KS_ROW_PIECES, pr = p - rn * KS_ROW_PIECES;
+            const int c = pr >= rn ? pr - rn : pr - rn + KS_ROW_PIECES;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(buf + 1024 * q),
+                                                     16, (uint32_t)(rn * a.w_s1 + 16 * c), 0, 0, 0);
+        }
+    };
+    dma_tile(0);
+    if (nt > 1) dma_tile(1);
+    const int cw = wave * (Q4K_BYTES / 16);  // the wave's super-block: pieces cw .. cw + 8 of a row
+    for (int t = 0; t < nt; ++t) {
+        // this wave's DMAs of tile t are done once at most those of tile t + 1 are outstanding (the
+        // activation loads and earlier stores are older still)
+        if (t + 1 < nt) {
+            if (ndma == 3) __builtin_amdgcn_s_waitcnt(3 | 0x0F70);
+            else __builtin_amdgcn_s_waitcnt(2 | 0x0F70);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0 | 0x0F70);
+        }
+        lds_barrier();  // every wave's DMAs of tile t have landed
+        const uint8_t *buf = tiles[t % NBUF];
+        Q4kLaneBlock w;
+        w.hdr = *(const uint4 *)(buf + 16 * ks_pos(n, cw));
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) w.qw[s4] = *(const uint4 *)(buf + 16 * ks_pos(n, cw + 1 + 2 * s4 + (g & 1)));
+        const bool rv = r0 + 16 * t + n < a.nrows;
+        Q4kPlanes P;
+        q4k_planes(w, rv, P);
+        v4f acc[MT];
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct) {
+            acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+            if (ct < ntile) q4k_tile_mma(P, act[ct], acc[ct]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct)
+            if (ct < ntile) red[wave][ct][lane] = acc[ct];
+        lds_barrier();
+        // element x of the tile (row n = x % 16 fastest, so 16 lanes store 16 consecutive floats)
+        for (int x = threadIdx.x; x < ntile * 256; x += W * 64) {
+            const int nn = x & 15, i4 = (x >> 4) & 3, gg = (x >> 6) & 3, ct = x >> 8;
+            float sum = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < W; ++w2) sum += red[w2][ct][nn + 16 * gg][i4];
+            const int col = 16 * ct + 4 * gg + i4;
+            const int64_t r = r0 + 16 * t + nn;
+            if (col < nvalid && r < a.nrows) a.dst[col_dst[col] + r] = sum;
+        }
+        // tile t + 2 goes into the buffer of tile t - 1, which every wave finished reading before the
+        // first barrier of this tile
+        if (t + 2 < nt) dma_tile(t + 2);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Decode-size routing (n_used * T <= SMALL_MAX_SLOTS): no routing pass. grid.y walks the slots; the
 // workgroup of a slot owns its expert when the slot is the expert's first occurrence, gathers every
@@ -719,7 +834,10 @@ hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream) {
         // the 32-bit range of a buffer resource)
         const size_t lds = mmid_act_lds(a.nb, a.chunk);
         const bool lds_act = lds <= MMID_ACT_LDS_MAX && a.q8_bytes < (1ll << 31);
-        if (lds_act) {
+        if (a.nb == KS_NB && mt <= 2 && (int64_t)16 * a.w_s1 < (1ll << 31)) {
+            if (mt == 1) k_mmid_ksplit_q4k<1><<<grid, MMID_SK_WAVES * 64, 0, stream>>>(a);
+            else k_mmid_ksplit_q4k<2><<<grid, MMID_SK_WAVES * 64, 0, stream>>>(a);
+        } else if (lds_act) {
             if (mt == 1) k_mmid_mfma_q4k_lds<1><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
             else if (mt == 2) k_mmid_mfma_q4k_lds<2><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
             else k_mmid_mfma_q4k_lds<4><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
