@@ -110,11 +110,13 @@ def test_gemv_columns(gpu, tname, m):
 
 
 @pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
-def test_gemv_broadcast_and_strides(gpu, tname):
-    """a [K, N, 2] broadcast over b [K, M, 4] (i02 = i12 / 2); b rows strided; dst a strided view."""
-    _case(f"{tname} broadcast")
+@pytest.mark.parametrize("m", [3, 4, 20])
+def test_gemv_broadcast_and_strides(gpu, tname, m):
+    """a [K, N, 2] broadcast over b [K, M, 4] (i02 = i12 / 2); b rows strided; dst a strided view. Q4_K at
+    4 and 20 columns takes the skinny kernel (F32 activations quantized in the workgroup, then Q8_K)."""
+    _case(f"{tname} broadcast m={m}")
     ty = TYPES[tname]
-    k, n, m = 512, 40, 3
+    k, n = 512, 40
     w = make_weights(ty, k, n, 2, seed=5, device=gpu)
     xb = normal((4, m, k + 64), 6)
     xt = torch.from_numpy(xb).to(gpu)[:, :, 32:32 + k]
@@ -124,7 +126,7 @@ def test_gemv_broadcast_and_strides(gpu, tname):
     got = out_big.cpu().numpy()
     assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
     want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 32:32 + k]), ne2=2)
-    check(got[:, :, :n], want, f"{tname} broadcast")
+    check(got[:, :, :n], want, f"{tname} broadcast m={m}")
 
 
 @pytest.mark.parametrize("tname", ["q4_K", "q6_K"])
@@ -197,7 +199,7 @@ def test_q6_K_output_head_full_size(gpu, m):
     assert np.all(np.isfinite(y))
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 32])
+@pytest.mark.parametrize("m", [1, 2, 4, 16, 32])
 def test_attention_projections(gpu, m):
     """q_proj 2048->4096, k/v_proj 2048->512, o_proj 4096->2048, Q4_K, at decode batch m."""
     ty = ggml.Type.Q4_K

@@ -157,7 +157,13 @@ template <int W> __device__ __forceinline__ float group_sum(float v) {
 // the bytes equal the CPU's. The parallel argmax keeps the first occurrence: among equal |x| the
 // smaller element index wins, which is what the left-to-right strict > scan selects (one 64-bit
 // maximum over the wave by DPP and permlane exchanges).
-__device__ __forceinline__ void quantize_q8k_wave(const float (&v)[4], uint8_t *blkp) {
+struct Q8kLane {
+    uint32_t packed;  // the lane's four qs bytes
+    int sum4;         // their sum
+    float d;          // the block's d (every lane)
+};
+
+__device__ __forceinline__ Q8kLane q8k_quantize_lane(const float (&v)[4]) {
     const int lane = (int)(threadIdx.x & 63);
     float amax = 0.f, vmax = 0.f;
     int imax = 0x7fffffff;
@@ -186,11 +192,23 @@ __device__ __forceinline__ void quantize_q8k_wave(const float (&v)[4], uint8_t *
         }
         d = __fdiv_rn(1.f, iscale);
     }
-    *(uint32_t *)(blkp + Q8K_QS + 4 * lane) = packed;
+    return Q8kLane{packed, s, d};
+}
+
+// The sum of the 16 qs of the lane's quad (lanes 4 i .. 4 i + 3: bsums[i]), in every lane of the quad.
+__device__ __forceinline__ int q8k_quad_sum(int s) {
     s += dpp_i<0xB1>(s);  // quad_perm [1,0,3,2]
     s += dpp_i<0x4E>(s);  // quad_perm [2,3,0,1]
+    return s;
+}
+
+__device__ __forceinline__ void quantize_q8k_wave(const float (&v)[4], uint8_t *blkp) {
+    const int lane = (int)(threadIdx.x & 63);
+    const Q8kLane q = q8k_quantize_lane(v);
+    *(uint32_t *)(blkp + Q8K_QS + 4 * lane) = q.packed;
+    const int s = q8k_quad_sum(q.sum4);
     if ((lane & 3) == 0) *(int16_t *)(blkp + Q8K_BSUMS + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *(float *)blkp = d;
+    if (lane == 0) *(float *)blkp = q.d;
 }
 
 __device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }

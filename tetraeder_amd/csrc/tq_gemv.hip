@@ -55,7 +55,7 @@ template <int F, int NC, int LPR> constexpr int gemv_dma_act_bytes() {
 // plain read of as many bytes is fastest at 2-3 KB in flight per wave too).
 constexpr int GEMV_DMA_NS = 2;
 // Activation blocks per wave whose floats are loaded ahead of the weight fills (F32 activations are
-// quantized in the workgroup up to 16 column blocks: two per wave).
+// quantized in the workgroup up to 32 column blocks: four per wave, the first two loaded ahead).
 constexpr int GEMV_DMA_PRE = 2;
 
 // The same over contiguous rows through wave-private LDS slots (gemv_rows_dma).
