@@ -40,8 +40,10 @@ template <int F> __device__ __forceinline__ int act_perm(int e) {
     }
 }
 
-// bsums slots of lane u (int16 each, ACT_SLOTS per lane): Q4_K two 32-element sums (sub-blocks 2u and
-// 2u+1, each the sum of two Q8_K bsums); Q6_K the four 16-element bsums of its groups 8h + 2k + v.
+// bsums slots of lane u (ACT_SLOTS per lane): Q4_K two 32-element sums as int16 (sub-blocks 2u and
+// 2u+1, each the sum of two Q8_K bsums); Q6_K -32 times the four 16-element bsums of its groups
+// 8h + 2k + v as int32 (the codes' -32 offset, the start of each group's dot product), at byte
+// 16 u + 4 s of the column block's ACT_BS_BYTES.
 template <int F> struct ActSlots { static constexpr int n = F == FMT_Q4K ? 2 : 4; };
 // The Q8_K 16-element bsums index of slot s of lane u (Q6_K), or the first of the two summed (Q4_K).
 template <int F> __device__ __forceinline__ int act_bs_src(int u, int s) {
@@ -70,9 +72,10 @@ __device__ __forceinline__ void stage_activations(ColSrc col_src, int nb, int nc
         if (c < ncols) {
             const int16_t *bs = (const int16_t *)(col_src(c) + (size_t)b * Q8K_BYTES + Q8K_BSUMS);
             const int g = act_bs_src<F>(u, s);
-            v = F == FMT_Q4K ? bs[g] + bs[g + 1] : bs[g];
+            v = F == FMT_Q4K ? bs[g] + bs[g + 1] : -32 * bs[g];
         }
-        lds_bs[cb * (ACT_BS_BYTES / 2) + u * SLOTS + s] = (int16_t)v;
+        if (F == FMT_Q4K) lds_bs[cb * (ACT_BS_BYTES / 2) + u * SLOTS + s] = (int16_t)v;
+        else *(int32_t *)((uint8_t *)lds_bs + cb * ACT_BS_BYTES + 16 * u + 4 * s) = v;
     }
     for (int i = tid; i < NC * nb; i += nthr) {
         const int c = i / nb, b = i - c * nb;
@@ -127,7 +130,7 @@ __device__ __forceinline__ void wave_quantize_vals_to_lds(const float (&v)[4], i
         if ((lane & 7) == 0) bs[lane >> 3] = (int16_t)sum;
     } else if ((lane & 3) == 0) {
         const int k = lane >> 2, h = k >> 3, s = (k & 7) >> 1, vv = k & 1;
-        bs[(2 * h + vv) * ActSlots<F>::n + s] = (int16_t)sum;
+        *(int32_t *)((uint8_t *)bs + 16 * (2 * h + vv) + 4 * s) = -32 * sum;
     }
     if (lane == 0) lds_d[cb] = d;
 }
@@ -161,7 +164,7 @@ __device__ __forceinline__ void zero_columns(int ncols, int nb, uint8_t *lds_qs,
     for (int i = ncols * nb * 64 + threadIdx.x; i < NC * nb * 64; i += blockDim.x)
         *(uint32_t *)(lds_qs + (i >> 6) * ACT_QS_PITCH + 4 * (i & 63)) = 0;
     for (int i = ncols * nb * 16 + threadIdx.x; i < NC * nb * 16; i += blockDim.x)
-        lds_bs[(i >> 4) * (ACT_BS_BYTES / 2) + (i & 15)] = 0;
+        *(int32_t *)((uint8_t *)lds_bs + (i >> 4) * ACT_BS_BYTES + 4 * (i & 15)) = 0;
 }
 
 // Stages NC columns given as F32 rows (column c starts at col_f32(c), nb*256 floats; zeros for c >=
@@ -222,10 +225,10 @@ template <> struct Item<FMT_Q6K> {
 };
 
 // One lane's activation operands of one column and super-block: its 64 Q8_K bytes, its bsums slots (Q4_K
-// the first dword: two 32-element sums; Q6_K both: four 16-element sums) and the block's d.
+// the first dword: two 32-element sums; Q6_K all four: -32 times four 16-element sums) and the block's d.
 struct ActOps {
     uint4 y0, y1, y2, y3;
-    uint2 bs;
+    uint4 bs;
     float d;
 };
 
@@ -237,9 +240,12 @@ __device__ __forceinline__ ActOps act_ops(const uint8_t *lds_qs, const int16_t *
     o.y0 = *(const uint4 *)(y), o.y1 = *(const uint4 *)(y + 16);
     o.y2 = *(const uint4 *)(y + 32), o.y3 = *(const uint4 *)(y + 48);
     if (F == FMT_Q4K) {
-        o.bs = uint2{*(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2), 0u};
+        o.bs = uint4{*(const uint32_t *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 2), 0u, 0u, 0u};
     } else {
-        o.bs = *(const uint2 *)(lds_bs + cb * (ACT_BS_BYTES / 2) + u * 4);
+        // two 8-byte reads (a column block's slots start 8-byte aligned)
+        const uint2 *p = (const uint2 *)((const uint8_t *)lds_bs + cb * ACT_BS_BYTES + 16 * u);
+        const uint2 lo = p[0], hi = p[1];
+        o.bs = uint4{lo.x, lo.y, hi.x, hi.y};
     }
     o.d = lds_d[cb];
     return o;
@@ -336,15 +342,13 @@ __device__ __forceinline__ void compute_item_ops(const Item<FMT_Q6K> &it, int u,
     for (int col = 0; col < NC; ++col) {
         const ActOps o = act(col);
         const uint4 y0 = o.y0, y1 = o.y1, y2 = o.y2, y3 = o.y3;
-        const int S0 = dot4(c0[3], y0.w, dot4(c0[2], y0.z, dot4(c0[1], y0.y, dot4(c0[0], y0.x, 0))));
-        const int S1 = dot4(c1[3], y1.w, dot4(c1[2], y1.z, dot4(c1[1], y1.y, dot4(c1[0], y1.x, 0))));
-        const int S2 = dot4(c2[3], y2.w, dot4(c2[2], y2.z, dot4(c2[1], y2.y, dot4(c2[0], y2.x, 0))));
-        const int S3 = dot4(c3[3], y3.w, dot4(c3[2], y3.z, dot4(c3[1], y3.y, dot4(c3[0], y3.x, 0))));
-        const uint2 bsw = o.bs;
-        const int corr = mad24(sc0, (int)(int16_t)(bsw.x & 0xffffu),
-                               mad24(sc1, (int)(int16_t)(bsw.x >> 16),
-                                     mad24(sc2, (int)(int16_t)(bsw.y & 0xffffu), mul24(sc3, (int)(int16_t)(bsw.y >> 16)))));
-        const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mad24(sc3, S3, mul24(-32, corr)))));
+        // each group's dot product starts from -32 times its bsum (the codes' offset)
+        const uint4 bsw = o.bs;
+        const int S0 = dot4(c0[3], y0.w, dot4(c0[2], y0.z, dot4(c0[1], y0.y, dot4(c0[0], y0.x, (int)bsw.x))));
+        const int S1 = dot4(c1[3], y1.w, dot4(c1[2], y1.z, dot4(c1[1], y1.y, dot4(c1[0], y1.x, (int)bsw.y))));
+        const int S2 = dot4(c2[3], y2.w, dot4(c2[2], y2.z, dot4(c2[1], y2.y, dot4(c2[0], y2.x, (int)bsw.z))));
+        const int S3 = dot4(c3[3], y3.w, dot4(c3[2], y3.z, dot4(c3[1], y3.y, dot4(c3[0], y3.x, (int)bsw.w))));
+        const int isum = mad24(sc0, S0, mad24(sc1, S1, mad24(sc2, S2, mul24(sc3, S3))));
         acc.v[col] += (o.d * d) * (float)isum;
     }
 }
