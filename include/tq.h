@@ -119,8 +119,9 @@ size_t tq_mul_mat_id_workspace_size(const tq_tensor *as, const tq_tensor *b, con
  * ids[j, t] < 0 reads no weights and writes an exact zero row (patch 0004,
  * patches/0004-cuda-mul-mat-id-skip-negative.patch:116-137,214-253); ids >= n_expert are undefined
  * behaviour in ggml and are written as zero rows here. Each expert's weights are read once per call
- * for all the tokens routed to it; the routing is compacted on the device (no host copy of ids,
- * unlike the generic path at patches/0004:12-79). Replaces the GPU backend's MUL_MAT_ID for
+ * for all the tokens routed to it (above 256 slots once per chunk of up to 32 or 64 of its tokens);
+ * the routing is compacted on the device (no host copy of ids, unlike the generic path at
+ * patches/0004:12-79). Replaces the GPU backend's MUL_MAT_ID for
  * Context::mul_mat_id (crates/ggml-sys/src/ggml/context.rs:320-336). */
 int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids, tq_tensor *dst, void *workspace,
                   size_t workspace_size, void *stream);
