@@ -204,19 +204,26 @@ constexpr int64_t MMQ_MIN_COLS = 64;
 // Q4_K from 4 to 64 columns: the skinny MFMA kernel (on MI355X q_proj 2048 -> 4096 at 4 / 16 / 32 / 64
 // columns: 8.1 / 8.5 / 10.0 / 13.1 us against 9.2 / 19.3 / 34.9 us for 8-column GEMV launches and 37.1 us
 // for the prefill kernel at 64).
+// F32 activations of 4 columns and at most 32 column blocks stay on the GEMV, which quantizes them in
+// its workgroups (q_proj 2048 -> 4096 at 4 columns: 6.8 us against 7.35 us for the Q8_K launch and the
+// skinny kernel; a Q8_K b keeps the skinny kernel, the faster of the two without the launch).
 constexpr int64_t SKINNY_MIN_COLS = 4, SKINNY_MAX_COLS = 64;
 
-static bool use_skinny(int type, int64_t ncols) {
+static bool skinny_columns(int type, int64_t ncols) {
     return ncols >= SKINNY_MIN_COLS && ncols <= SKINNY_MAX_COLS && skinny_supported(type, ncols);
 }
-static bool use_mmq(int type, int64_t ncols) { return ncols >= MMQ_MIN_COLS && !use_skinny(type, ncols); }
+static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
+    if (f32 && ncols <= 4 && ncols * nb <= 32) return false;
+    return skinny_columns(type, ncols);
+}
+static bool use_mmq(int type, int64_t ncols) { return ncols >= MMQ_MIN_COLS && !skinny_columns(type, ncols); }
 
 
 // Decode-size F32 activations are quantized inside the GEMV workgroups (no workspace, one launch): up
 // to 32 column blocks per workgroup (o_proj 4096 -> 2048 at 2 columns: 6.3 us against 7.6 us with a
 // quantization launch of its own on MI355X).
 static bool quantize_in_workgroup(int type, int64_t ncols, int nb) {
-    return !use_mmq(type, ncols) && !use_skinny(type, ncols) && ncols * nb <= 32;
+    return !use_mmq(type, ncols) && !use_skinny(type, ncols, nb, true) && ncols * nb <= 32;
 }
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
@@ -324,7 +331,7 @@ static int check_mul_mat(const tq_tensor *a, const tq_tensor *b, const tq_tensor
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
     const int nb = (int)(a->ne[0] / QK);
     const bool mmq = use_mmq(a->type, b->ne[1]);
-    const bool skinny = use_skinny(a->type, b->ne[1]);
+    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32);
     const int nc_max = nb ? (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb)) : 8;
     if (!mmq && !skinny && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
     if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
@@ -339,7 +346,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     const int nb = (int)(a->ne[0] / QK);
     const bool pre_quantized = b->type == TQ_TYPE_Q8_K;
     const bool mmq = use_mmq(a->type, b->ne[1]);
-    const bool skinny = use_skinny(a->type, b->ne[1]);
+    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32);
     const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
 
     hipStream_t s = (hipStream_t)stream;
