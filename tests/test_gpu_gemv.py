@@ -223,3 +223,58 @@ def test_q4_K_batched_decode_shapes(gpu, k, n, m):
     y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
     want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
     check(y, want, f"q4_K k={k} n={n} m={m}")
+
+
+@pytest.mark.parametrize("n,m", [(17, 4), (300, 7), (4101, 13), (2048, 16), (1000, 33), (512, 64)])
+def test_q6_K_batched_decode_shapes(gpu, n, m):
+    """Q6_K at K = 2048 with 4..64 columns runs the Q6_K MFMA kernel (16 columns per launch, up to 8 of
+    them quantized inside it): row counts that are no multiple of the 16-row tiles, fewer tiles than
+    workgroups and several tiles per workgroup, column counts that are no multiple of 4."""
+    _case(f"q6_K skinny n={n} m={m}")
+    ty = TYPES["q6_K"]
+    k = 2048
+    w = make_weights(ty, k, n, 1, seed=n + m, device=gpu)
+    x = normal((m, k), 11 * m + n)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q6_K k={k} n={n} m={m}")
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("m", [4, 13])
+def test_q6_K_skinny_broadcast_and_strides(gpu, m):
+    """The Q6_K MFMA kernel over batches: a [2048, 40, 2] broadcast over b [2048, m, 4] (i02 = i12 / 2),
+    b rows strided and 4-byte aligned only, dst a strided view whose padding must stay untouched."""
+    _case(f"q6_K skinny broadcast m={m}")
+    ty = TYPES["q6_K"]
+    k, n = 2048, 40
+    w = make_weights(ty, k, n, 2, seed=9, device=gpu)
+    xb = normal((4, m, k + 68), 10)
+    xt = torch.from_numpy(xb).to(gpu)[:, :, 33:33 + k]
+    out_big = torch.full((4, m, n + 8), float("nan"), device=gpu)
+    out = out_big[:, :, :n]
+    ggml.mul_mat(w, xt, out=out)
+    got = out_big.cpu().numpy()
+    assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 33:33 + k]), ne2=2)
+    check(got[:, :, :n], want, f"q6_K skinny broadcast m={m}")
+
+
+@pytest.mark.parametrize("m", [6, 40])
+def test_q6_K_skinny_dynamic_range_and_zero_columns(gpu, m):
+    """The Q6_K MFMA kernel with columns scaled over 1e-30 .. 1e30 and all-zero columns (Q8_K d = 0),
+    quantized inside the kernel (6 columns) and by the Q8_K pass (40)."""
+    _case(f"q6_K skinny dynamic range m={m}")
+    ty = TYPES["q6_K"]
+    k, n = 2048, 100
+    w = make_weights(ty, k, n, 1, seed=12, device=gpu)
+    x = normal((m, k), 13)
+    x *= (10.0 ** np.linspace(-30, 30, m)).astype(np.float32)[:, None]
+    x[1] = 0.0
+    x[m - 2] = 0.0
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    assert np.all(y[1] == 0) and np.all(y[m - 2] == 0)
+    for i in range(m):  # each column against its own magnitude
+        if i not in (1, m - 2):
+            check(y[i], want[i], f"q6_K column {i}")

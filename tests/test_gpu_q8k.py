@@ -102,3 +102,22 @@ def test_in_kernel_quantization_matches_the_pass(gpu, tname, kind):
         torch.cuda.synchronize()
         assert got.numel() == want.numel() == m * 512
         assert torch.equal(got.reshape(-1), want.reshape(-1)), f"m={m}: in-kernel Q8_K differs from the pass"
+
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "zero_blocks", "dup_max", "extreme"])
+def test_q6_K_mfma_in_kernel_quantization_matches_the_pass(gpu, kind):
+    """The Q6_K MFMA kernel (K = 2048, 4..8 columns) quantizes F32 activations in its waves; its outputs
+    equal, bit for bit, those of the same kernel over the Q8_K pass's bytes."""
+    from tests.test_gpu_gemv import make_weights
+    _case(f"q6_K mfma in-kernel {kind}")
+    k = 2048
+    w = make_weights(ggml.Type.Q6_K, k, 700, 1, seed=23, device=gpu)
+    for m in (4, 6, 8):
+        x = torch.from_numpy(np.ascontiguousarray(_inputs(kind, m, k, 60 + m))).to(gpu)
+        assert ggml.mul_mat_workspace_size(w, x) == 0  # the in-kernel path
+        got = ggml.mul_mat(w, x)
+        xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
+        want = ggml.mul_mat(w, xq)
+        torch.cuda.synchronize()
+        assert torch.equal(got.reshape(-1), want.reshape(-1)), f"m={m}: in-kernel Q8_K differs from the pass"

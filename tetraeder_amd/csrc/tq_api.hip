@@ -216,14 +216,43 @@ static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
     if (f32 && ncols <= 4 && ncols * nb <= 32) return false;
     return skinny_columns(type, ncols);
 }
-static bool use_mmq(int type, int64_t ncols) { return ncols >= MMQ_MIN_COLS && !skinny_columns(type, ncols); }
 
+// Q6_K at K = 2048 from 4 to 32 columns: the Q6_K MFMA kernel, 16 columns per launch, F32 activations
+// of up to 8 columns quantized inside it (more get the Q8_K pass: every workgroup would repeat it);
+// from 33 columns the prefill kernel (on MI355X, the 151936 x 2048 head at 4 / 8 / 16 / 32 / 64 columns:
+// 54 / 67 / 84 / 165 / 328 us against 59 / 95 / 185 / 371 us for 8-column GEMV launches and 189 us for
+// the prefill kernel at 64).
+#ifndef TQ_SKINNY6_MIN_COLS
+#define TQ_SKINNY6_MIN_COLS 4
+#endif
+constexpr int64_t SKINNY6_MIN_COLS = TQ_SKINNY6_MIN_COLS, SKINNY6_MAX_COLS = 32, SKINNY6_COLS_PER_LAUNCH = 16,
+                  SKINNY6_QUANT_MAX_COLS = 8;
+static GemvArgs weight_args(const tq_tensor *a) {
+    GemvArgs g{};
+    g.w = (const uint8_t *)a->data;
+    g.nrows = a->ne[1];
+    g.nb = (int32_t)(a->ne[0] / QK);
+    g.row_stride = (int64_t)a->nb[1];
+    g.w_s2 = (int64_t)a->nb[2];
+    g.w_s3 = (int64_t)a->nb[3];
+    return g;
+}
+static bool skinny6_shape(const tq_tensor *a) { return a->type == TQ_TYPE_Q6_K && skinny_q6k_supported(weight_args(a)); }
+static bool use_skinny6(const tq_tensor *a, int64_t ncols) {
+    return ncols >= SKINNY6_MIN_COLS && ncols <= SKINNY6_MAX_COLS && skinny6_shape(a);
+}
+
+static bool use_mmq(const tq_tensor *a, int64_t ncols) {
+    const int64_t min_cols = ncols > SKINNY6_MAX_COLS && skinny6_shape(a) ? SKINNY6_MAX_COLS + 1 : MMQ_MIN_COLS;
+    return ncols >= min_cols && !skinny_columns(a->type, ncols) && !use_skinny6(a, ncols);
+}
 
 // Decode-size F32 activations are quantized inside the GEMV workgroups (no workspace, one launch): up
 // to 32 column blocks per workgroup (o_proj 4096 -> 2048 at 2 columns: 6.3 us against 7.6 us with a
-// quantization launch of its own on MI355X).
-static bool quantize_in_workgroup(int type, int64_t ncols, int nb) {
-    return !use_mmq(type, ncols) && !use_skinny(type, ncols, nb, true) && ncols * nb <= 32;
+// quantization launch of its own on MI355X); the Q6_K MFMA kernel quantizes up to 8 columns itself.
+static bool quantize_in_workgroup(const tq_tensor *a, int64_t ncols, int nb) {
+    if (use_skinny6(a, ncols)) return ncols <= SKINNY6_QUANT_MAX_COLS;
+    return !use_mmq(a, ncols) && !use_skinny(a->type, ncols, nb, true) && ncols * nb <= 32;
 }
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
@@ -231,10 +260,10 @@ static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8
 // MUL_MAT's workspace: the Q8_K copy of an F32 b (none when b is Q8_K already or is quantized inside the
 // GEMV workgroups), then the partial tiles of a prefill launch split along k.
 static size_t mul_mat_q8_part(const tq_tensor *a, const tq_tensor *b) {
-    return b->type == TQ_TYPE_F32 && !quantize_in_workgroup(a->type, b->ne[1], (int)(a->ne[0] / QK)) ? q8_bytes(b) : 0;
+    return b->type == TQ_TYPE_F32 && !quantize_in_workgroup(a, b->ne[1], (int)(a->ne[0] / QK)) ? q8_bytes(b) : 0;
 }
 static size_t mul_mat_split_part(const tq_tensor *a, const tq_tensor *b) {
-    if (!use_mmq(a->type, b->ne[1])) return 0;
+    if (!use_mmq(a, b->ne[1])) return 0;
     return align_up(mmq_split_bytes(a->type, b->ne[1], a->ne[1], (int)(a->ne[0] / QK), (int)(b->ne[2] * b->ne[3])), 256);
 }
 
@@ -330,8 +359,8 @@ static int check_mul_mat(const tq_tensor *a, const tq_tensor *b, const tq_tensor
         return fail(TQ_STATUS_FAILED, "dst shape is not [a.ne1, b.ne1, b.ne2, b.ne3]");
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
     const int nb = (int)(a->ne[0] / QK);
-    const bool mmq = use_mmq(a->type, b->ne[1]);
-    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32);
+    const bool mmq = use_mmq(a, b->ne[1]);
+    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32) || use_skinny6(a, b->ne[1]);
     const int nc_max = nb ? (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb)) : 8;
     if (!mmq && !skinny && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
     if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
@@ -345,15 +374,16 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     if (nrows(b) == 0 || a->ne[1] == 0) return TQ_STATUS_SUCCESS;
     const int nb = (int)(a->ne[0] / QK);
     const bool pre_quantized = b->type == TQ_TYPE_Q8_K;
-    const bool mmq = use_mmq(a->type, b->ne[1]);
+    const bool mmq = use_mmq(a, b->ne[1]);
     const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32);
+    const bool skinny6 = use_skinny6(a, b->ne[1]);
     const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
 
     hipStream_t s = (hipStream_t)stream;
     void *q8 = b->data;
     // Small activations (decode) are quantized inside each GEMV workgroup, straight into LDS: one launch
     // instead of two. Larger ones get their own quantization pass first.
-    const bool in_wg = !pre_quantized && quantize_in_workgroup(a->type, b->ne[1], nb);
+    const bool in_wg = !pre_quantized && quantize_in_workgroup(a, b->ne[1], nb);
     const size_t q8_need = mul_mat_q8_part(a, b), split_need = mul_mat_split_part(a, b);
     uint8_t *ws = nullptr;
     if (q8_need + split_need) {
@@ -400,13 +430,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         if (skinny) return check_hip(launch_skinny(a->type, m, s), "skinny launch");
         return check_hip(launch_mmq(a->type, m, s), "mmq launch");
     }
-    GemvArgs g{};
-    g.w = (const uint8_t *)a->data;
-    g.nrows = a->ne[1];
-    g.nb = nb;
-    g.row_stride = (int64_t)a->nb[1];
-    g.w_s2 = (int64_t)a->nb[2];
-    g.w_s3 = (int64_t)a->nb[3];
+    GemvArgs g = weight_args(a);
     g.r2 = (int32_t)(b->ne[2] / a->ne[2]);
     g.r3 = (int32_t)(b->ne[3] / a->ne[3]);
     g.ne12 = (int32_t)b->ne[2];
@@ -424,10 +448,13 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         g.b_s3 = (int64_t)(b->nb[3] / 4);
         g.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0 && b->nb[3] % 16 == 0;
     }
-    for (int64_t c0 = 0; c0 < b->ne[1]; c0 += nc_max) {
+    const int64_t per_launch = skinny6 ? SKINNY6_COLS_PER_LAUNCH : nc_max;
+    for (int64_t c0 = 0; c0 < b->ne[1]; c0 += per_launch) {
         g.col0 = (int32_t)c0;
-        g.ncols = (int32_t)std::min<int64_t>(nc_max, b->ne[1] - c0);
-        if ((rc = check_hip(launch_gemv(a->type, g, s), "gemv launch"))) return rc;
+        g.ncols = (int32_t)std::min<int64_t>(per_launch, b->ne[1] - c0);
+        if ((rc = check_hip(skinny6 ? launch_skinny_q6k(g, s) : launch_gemv(a->type, g, s),
+                            skinny6 ? "skinny q6_K launch" : "gemv launch")))
+            return rc;
     }
     return TQ_STATUS_SUCCESS;
 }
