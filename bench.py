@@ -52,6 +52,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--moe-tokens", type=int, default=0, help="with --only moe: run just this token count")
+    p.add_argument("--cols", type=int, default=1, help="with --only head: activation columns (decode batch)")
     p.add_argument("--only", choices=["gemv", "head", "copy", "moe", "prefill", "secondary", "slots", "ranks", "cpu"],
                    default=None,
                    help="profiling runs: 'gemv' replays the headline graph of --steps Q4_K 4096 x 4096 launches, "
@@ -408,15 +409,15 @@ def main():
         log(f"replayed a graph of {args.steps} Q4_K 4096x4096 GEMV launches")
         return
     if args.only == "head":
-        ty, k, n = ggml.Type.Q6_K, 2048, 151936
+        ty, k, n, m = ggml.Type.Q6_K, 2048, 151936, args.cols
         W = make_weights(ggml, torch, ty, k, n, 2, seed=1, dev=dev)
-        x = torch.randn((1, k), generator=torch.Generator(device=dev).manual_seed(2), device=dev)
-        out = torch.empty((1, n), device=dev)
-        xq = ggml.QTensor(ggml.Type.Q8_K, (k, 1), ggml.quantize_q8_K(x).view(-1))
+        x = torch.randn((m, k), generator=torch.Generator(device=dev).manual_seed(2), device=dev)
+        out = torch.empty((m, n), device=dev)
+        xq = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(x).view(-1))
         for i in range(args.steps):
             ggml.mul_mat(W[i & 1], xq, out=out)
         torch.cuda.synchronize()
-        log(f"ran {args.steps} Q6_K head GEMV launches")
+        log(f"ran {args.steps} Q6_K head MUL_MAT launches at {m} columns")
         return
     if args.only == "moe":
         print(json.dumps(bench_moe(ggml, torch, np, dev, tokens=(args.moe_tokens,) if args.moe_tokens else None)))
