@@ -181,10 +181,10 @@ def test_device_quantizer_round_trip(gpu):
     assert errs[0] < 0.15 and errs[1] < 0.05 and errs[1] < errs[0], errs
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 2, 4])
 def test_q6_K_output_head_full_size(gpu, m):
-    """The Q6_K output head 151936 x 2048 at its real size; a seeded sample of 2048 rows against the
-    oracle (the whole matrix is 255 MB)."""
+    """The Q6_K output head 151936 x 2048 at its real size (the GEMV at 1 column, the Q6_K MFMA kernel at
+    2 and 4); a seeded sample of 2048 rows against the oracle (the whole matrix is 255 MB)."""
     _case(f"q6_K head m={m}")
     ty = ggml.Type.Q6_K
     k, n = 2048, 151936
@@ -225,11 +225,13 @@ def test_q4_K_batched_decode_shapes(gpu, k, n, m):
     check(y, want, f"q4_K k={k} n={n} m={m}")
 
 
-@pytest.mark.parametrize("n,m", [(17, 4), (300, 7), (4101, 13), (2048, 16), (1000, 33), (512, 64)])
+@pytest.mark.parametrize("n,m", [(17, 3), (17, 4), (300, 7), (4101, 13), (2048, 16), (5000, 20), (1000, 32), (1000, 33),
+                                 (512, 64)])
 def test_q6_K_batched_decode_shapes(gpu, n, m):
-    """Q6_K at K = 2048 with 4..64 columns runs the Q6_K MFMA kernel (16 columns per launch, up to 8 of
-    them quantized inside it): row counts that are no multiple of the 16-row tiles, fewer tiles than
-    workgroups and several tiles per workgroup, column counts that are no multiple of 4."""
+    """Q6_K at K = 2048 with 3..32 columns runs the Q6_K MFMA kernel (16 columns per launch, up to 8 of
+    them quantized inside it), from 33 the prefill kernel: row counts that are no multiple of the 16-row
+    tiles, fewer tiles than workgroups and several tiles per workgroup, column counts that are no
+    multiple of 4."""
     _case(f"q6_K skinny n={n} m={m}")
     ty = TYPES["q6_K"]
     k = 2048

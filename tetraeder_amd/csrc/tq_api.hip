@@ -217,16 +217,19 @@ static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
     return skinny_columns(type, ncols);
 }
 
-// Q6_K at K = 2048 from 4 to 32 columns: the Q6_K MFMA kernel, 16 columns per launch, F32 activations
-// of up to 8 columns quantized inside it (more get the Q8_K pass: every workgroup would repeat it);
-// from 33 columns the prefill kernel (on MI355X, the 151936 x 2048 head at 4 / 8 / 16 / 32 / 64 columns:
-// 54 / 67 / 84 / 165 / 328 us against 59 / 95 / 185 / 371 us for 8-column GEMV launches and 189 us for
-// the prefill kernel at 64).
+// Q6_K at K = 2048 from 3 to 32 columns (2 on matrices of 64K rows and more): the Q6_K MFMA kernel, 16
+// columns per launch, F32 activations of up to 8 columns quantized inside it (more get the Q8_K pass:
+// every workgroup would repeat it); from 33 columns the prefill kernel. On MI355X, ops on F32 columns
+// in graphs, against the GEMV: the 151936 x 2048 head at 2 / 3 / 4 / 8 columns 45.0 / 43.5 / 44.0 /
+// 53.2 us against 46.8 / 57.1 / 58.9 / 97.3; 4096 rows 5.9 / 6.2 / 6.5 / 8.9 against 5.1 / 6.4 / 6.9 /
+// 11.2; 512 rows 5.4 / 5.7 / 6.0 / 8.3 against 4.6 / 6.0 / 6.5 / 10.3. The head at 16 / 32 / 64 Q8_K
+// columns: 63.6 / 127 / 328 us against 185 / 371 us for 8-column GEMV launches and 189 us for the
+// prefill kernel at 64.
 #ifndef TQ_SKINNY6_MIN_COLS
-#define TQ_SKINNY6_MIN_COLS 4
+#define TQ_SKINNY6_MIN_COLS 3
 #endif
 constexpr int64_t SKINNY6_MIN_COLS = TQ_SKINNY6_MIN_COLS, SKINNY6_MAX_COLS = 32, SKINNY6_COLS_PER_LAUNCH = 16,
-                  SKINNY6_QUANT_MAX_COLS = 8;
+                  SKINNY6_QUANT_MAX_COLS = 8, SKINNY6_TWO_COL_MIN_ROWS = 65536;
 static GemvArgs weight_args(const tq_tensor *a) {
     GemvArgs g{};
     g.w = (const uint8_t *)a->data;
@@ -239,7 +242,9 @@ static GemvArgs weight_args(const tq_tensor *a) {
 }
 static bool skinny6_shape(const tq_tensor *a) { return a->type == TQ_TYPE_Q6_K && skinny_q6k_supported(weight_args(a)); }
 static bool use_skinny6(const tq_tensor *a, int64_t ncols) {
-    return ncols >= SKINNY6_MIN_COLS && ncols <= SKINNY6_MAX_COLS && skinny6_shape(a);
+    const bool cols = (ncols >= SKINNY6_MIN_COLS || (ncols == 2 && a->ne[1] >= SKINNY6_TWO_COL_MIN_ROWS)) &&
+                      ncols <= SKINNY6_MAX_COLS;
+    return cols && skinny6_shape(a);
 }
 
 static bool use_mmq(const tq_tensor *a, int64_t ncols) {
