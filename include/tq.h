@@ -88,8 +88,9 @@ int tq_supports_op(int op, int type_a, int type_b);
 int tq_quantize_q8_K(const tq_tensor *src, void *dst, void *stream);
 
 /* Workspace bytes tq_mul_mat needs for these operands: the Q8_K copy of an F32 b (none for a Q8_K b or a
- * decode-size b, quantized inside the GEMV workgroups) and, for a prefill-size b whose output has too few
- * tiles to fill the GPU, the partial output tiles of the split along k (0 when nothing is needed). */
+ * decode-size b, which the GEMV workgroups or the Q6_K MFMA kernel's waves quantize themselves) and, for
+ * a prefill-size b whose output has too few tiles to fill the GPU, the partial output tiles of the split
+ * along k (0 when nothing is needed). */
 size_t tq_mul_mat_workspace_size(const tq_tensor *a, const tq_tensor *b);
 
 /* dst = MUL_MAT(a, b), ggml semantics: a Q4_K/Q6_K [K, N, ne02, ne03], b F32 [K, M, ne12, ne13]
