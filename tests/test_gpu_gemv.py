@@ -243,13 +243,13 @@ def test_q6_K_batched_decode_shapes(gpu, n, m):
     assert np.all(np.isfinite(y))
 
 
-@pytest.mark.parametrize("m", [4, 13])
-def test_q6_K_skinny_broadcast_and_strides(gpu, m):
-    """The Q6_K MFMA kernel over batches: a [2048, 40, 2] broadcast over b [2048, m, 4] (i02 = i12 / 2),
-    b rows strided and 4-byte aligned only, dst a strided view whose padding must stay untouched."""
-    _case(f"q6_K skinny broadcast m={m}")
+@pytest.mark.parametrize("k,m", [(2048, 4), (2048, 13), (4096, 5), (4096, 11)])
+def test_q6_K_skinny_broadcast_and_strides(gpu, k, m):
+    """The Q6_K MFMA kernel over batches: a [k, 40, 2] broadcast over b [k, m, 4] (i02 = i12 / 2), b rows
+    strided and 4-byte aligned only, dst a strided view whose padding must stay untouched."""
+    _case(f"q6_K skinny broadcast k={k} m={m}")
     ty = TYPES["q6_K"]
-    k, n = 2048, 40
+    n = 40
     w = make_weights(ty, k, n, 2, seed=9, device=gpu)
     xb = normal((4, m, k + 68), 10)
     xt = torch.from_numpy(xb).to(gpu)[:, :, 33:33 + k]
@@ -259,7 +259,7 @@ def test_q6_K_skinny_broadcast_and_strides(gpu, m):
     got = out_big.cpu().numpy()
     assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
     want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 33:33 + k]), ne2=2)
-    check(got[:, :, :n], want, f"q6_K skinny broadcast m={m}")
+    check(got[:, :, :n], want, f"q6_K skinny broadcast k={k} m={m}")
 
 
 @pytest.mark.parametrize("m", [6, 40])
@@ -280,3 +280,18 @@ def test_q6_K_skinny_dynamic_range_and_zero_columns(gpu, m):
     for i in range(m):  # each column against its own magnitude
         if i not in (1, m - 2):
             check(y[i], want[i], f"q6_K column {i}")
+
+
+@pytest.mark.parametrize("n,m", [(17, 3), (300, 4), (4101, 8), (1000, 13), (2048, 32), (1000, 2)])
+def test_q6_K_k4096_batched_decode_shapes(gpu, n, m):
+    """Q6_K at K = 4096: the Q6_K MFMA kernel with two super-blocks per wave (8 columns per launch, the
+    activations staged in the second tile buffer), and the GEMV at 2 columns on a small matrix."""
+    _case(f"q6_K k=4096 n={n} m={m}")
+    ty = TYPES["q6_K"]
+    k = 4096
+    w = make_weights(ty, k, n, 1, seed=3 * n + m, device=gpu)
+    x = normal((m, k), 5 * m + n)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q6_K k={k} n={n} m={m}")
+    assert np.all(np.isfinite(y))

@@ -105,13 +105,13 @@ def test_in_kernel_quantization_matches_the_pass(gpu, tname, kind):
 
 
 
+@pytest.mark.parametrize("k", [2048, 4096])
 @pytest.mark.parametrize("kind", ["normal", "ties", "zero_blocks", "dup_max", "extreme"])
-def test_q6_K_mfma_in_kernel_quantization_matches_the_pass(gpu, kind):
-    """The Q6_K MFMA kernel (K = 2048, 4..8 columns) quantizes F32 activations in its waves; its outputs
-    equal, bit for bit, those of the same kernel over the Q8_K pass's bytes."""
+def test_q6_K_mfma_in_kernel_quantization_matches_the_pass(gpu, kind, k):
+    """The Q6_K MFMA kernel (K = 2048 and 4096, 4..8 columns) quantizes F32 activations in its waves; its
+    outputs equal, bit for bit, those of the same kernel over the Q8_K pass's bytes."""
     from tests.test_gpu_gemv import make_weights
-    _case(f"q6_K mfma in-kernel {kind}")
-    k = 2048
+    _case(f"q6_K mfma in-kernel {kind} k={k}")
     w = make_weights(ggml.Type.Q6_K, k, 700, 1, seed=23, device=gpu)
     for m in (4, 6, 8):
         x = torch.from_numpy(np.ascontiguousarray(_inputs(kind, m, k, 60 + m))).to(gpu)

@@ -217,9 +217,9 @@ static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
     return skinny_columns(type, ncols);
 }
 
-// Q6_K at K = 2048 from 3 to 32 columns (2 on matrices of 64K rows and more): the Q6_K MFMA kernel, 16
-// columns per launch, F32 activations of up to 8 columns quantized inside it (more get the Q8_K pass:
-// every workgroup would repeat it); from 33 columns the prefill kernel. On MI355X, ops on F32 columns
+// Q6_K at K = 2048 or 4096 from 3 to 32 columns (2 on matrices of 64K rows and more): the Q6_K MFMA
+// kernel, 16 (K = 2048) or 8 columns per launch, F32 activations of up to 8 columns quantized inside it
+// (more get the Q8_K pass: every workgroup would repeat it); from 33 columns the prefill kernel. On MI355X, ops on F32 columns
 // in graphs, against the GEMV: the 151936 x 2048 head at 2 / 3 / 4 / 8 columns 45.0 / 43.5 / 44.0 /
 // 53.2 us against 46.8 / 57.1 / 58.9 / 97.3; 4096 rows 5.9 / 6.2 / 6.5 / 8.9 against 5.1 / 6.4 / 6.9 /
 // 11.2; 512 rows 5.4 / 5.7 / 6.0 / 8.3 against 4.6 / 6.0 / 6.5 / 10.3. The head at 16 / 32 / 64 Q8_K
@@ -228,8 +228,8 @@ static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
 #ifndef TQ_SKINNY6_MIN_COLS
 #define TQ_SKINNY6_MIN_COLS 3
 #endif
-constexpr int64_t SKINNY6_MIN_COLS = TQ_SKINNY6_MIN_COLS, SKINNY6_MAX_COLS = 32, SKINNY6_COLS_PER_LAUNCH = 16,
-                  SKINNY6_QUANT_MAX_COLS = 8, SKINNY6_TWO_COL_MIN_ROWS = 65536;
+constexpr int64_t SKINNY6_MIN_COLS = TQ_SKINNY6_MIN_COLS, SKINNY6_MAX_COLS = 32, SKINNY6_QUANT_MAX_COLS = 8,
+                  SKINNY6_TWO_COL_MIN_ROWS = 65536;
 static GemvArgs weight_args(const tq_tensor *a) {
     GemvArgs g{};
     g.w = (const uint8_t *)a->data;
@@ -453,7 +453,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
         g.b_s3 = (int64_t)(b->nb[3] / 4);
         g.b_vec = (uintptr_t)b->data % 16 == 0 && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0 && b->nb[3] % 16 == 0;
     }
-    const int64_t per_launch = skinny6 ? SKINNY6_COLS_PER_LAUNCH : nc_max;
+    const int64_t per_launch = skinny6 ? skinny_q6k_cols_per_launch(nb) : nc_max;
     for (int64_t c0 = 0; c0 < b->ne[1]; c0 += per_launch) {
         g.col0 = (int32_t)c0;
         g.ncols = (int32_t)std::min<int64_t>(per_launch, b->ne[1] - c0);

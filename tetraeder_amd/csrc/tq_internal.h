@@ -98,9 +98,11 @@ hipError_t launch_mmq_tile_q6k(const MmqArgs &a, hipStream_t stream);
 using SkinnyArgs = MmqArgs;
 bool skinny_supported(int type, int64_t ncols);
 hipError_t launch_skinny(int type, const SkinnyArgs &a, hipStream_t stream);
-// The same for Q6_K weights at K = 2048 (rows 16-byte aligned), 1 <= ncols <= 16 per launch (col0 ..
-// col0 + ncols - 1 of the GemvArgs columns); F32 activations (b set) are quantized inside the kernel.
+// The same for Q6_K weights at K = 2048 or 4096 (rows 16-byte aligned), 1 <= ncols <=
+// skinny_q6k_cols_per_launch(nb) per launch (col0 .. col0 + ncols - 1 of the GemvArgs columns); F32
+// activations (b set) are quantized inside the kernel.
 bool skinny_q6k_supported(const GemvArgs &a);
+int skinny_q6k_cols_per_launch(int nb);
 hipError_t launch_skinny_q6k(const GemvArgs &a, hipStream_t stream);
 constexpr size_t gemv_lds_per_col_block() { return ACT_QS_PITCH + ACT_BS_BYTES + 4; }
 constexpr size_t gemv_max_lds() { return 64 * 1024; }

@@ -158,8 +158,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_direct(SkinnyArgs 
 }
 
 // ------------------------------------------------------------------------------------------------
-// Q6_K at K = 2048 for 1..16 columns per launch (ggml's vec_dot_q6_K_q8_K per super-block:
-//   d * d_y * sum_G sc_G * sum_{k in G} (q_k - 32) y_k,  16 groups G of 16 weights, signed 8-bit sc_G).
+// Q6_K at K = 2048 (1..16 columns per launch) and K = 4096 (1..8) (ggml's vec_dot_q6_K_q8_K per
+// super-block: d * d_y * sum_G sc_G * sum_{k in G} (q_k - 32) y_k, 16 groups G of 16 weights, signed
+// 8-bit sc_G).
 // sc_G * q does not fit a byte, so the scales stay out of the MFMA: its 16 output rows are 4 activation
 // columns x 4 scale groups. In a 16x16x64 step j the four lane groups g (= 2h + v, the k-slots 16 g ..
 // +15) hold the 16 codes of group G(j, g) = 8 h + 2 j + v of their row (one of the four 16-byte code
@@ -170,39 +171,44 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_direct(SkinnyArgs 
 // column's group sums (bsums), which is the codes' offset. The k-split is ggml's: sums per group in
 // int32, one fp32 multiply-add per super-block and column.
 // Grid: a few workgroups per CU (persistent), each over a contiguous range of 16-row tiles; wave w owns
-// super-block w of every tile and stages the activations of that super-block (quantized from F32 in
-// the wave, or copied from Q8_K) in LDS once. The tiles (16 rows x 1680 bytes, contiguous) come into
-// LDS by wave-wide LDS DMAs two tiles ahead in three buffers, rows padded to 107 pieces of 16 bytes
-// (107 n mod 16 is odd, so the same dword of 16 rows falls in 16 different bank groups); the waves'
-// partial sums of a tile meet in LDS.
+// super-blocks w + 8 i (i < NBW, NBW = K / 2048) of every tile and stages the activations of those
+// super-blocks (quantized from F32 in the wave, or copied from Q8_K) once. The tiles (16 rows x
+// 1680 NBW bytes, contiguous) come into LDS by wave-wide non-temporal LDS DMAs, NBUF - 1 tiles ahead,
+// rows padded to an odd number of 16-byte pieces (so the same dword of 16 rows falls in 16 different
+// bank groups); the waves' partial sums of a tile meet in LDS after the next tile's barrier.
 // ------------------------------------------------------------------------------------------------
-constexpr int S6_NB = 8;                               // super-blocks per row (K = 2048)
-constexpr int S6_ROW_PIECES = S6_NB * Q6K_BYTES / 16;  // 16-byte pieces of a row (105)
-constexpr int S6_PITCH = 107;                          // LDS pieces per staged row
-constexpr int S6_TILE = 16 * S6_PITCH * 16;            // LDS bytes of a staged tile
-constexpr int S6_DMAS = (16 * S6_PITCH + 63) / 64;     // wave-wide DMAs per tile (27)
-constexpr int S6_QP = 272;                             // LDS bytes per staged activation block (qs + pad)
-static_assert(SK_WAVES == S6_NB, "one super-block per wave");
-static_assert(S6_ROW_PIECES * 16 == S6_NB * Q6K_BYTES, "whole pieces per row");
+constexpr int S6_QP = 272;  // LDS bytes per staged activation block (qs + pad)
 
-// LDS layout for S sets of 4 columns: NBUF tile buffers, then wave w's activation blocks: qs of column
-// k at ACT + (w (NCOL + 1) + k) S6_QP, column NCOL all zeros (the A operand's zero lanes read it); CIN:
-// per column k and step j, int4 {-32 bsum of group G(j, i), i = 0..3}; DACT: d of column k; RED: the
-// waves' partial sums of two tiles (float [tile parity][wave][set][64]).
-template <int S, int NBUF_> struct S6Layout {
-    static constexpr int NCOL = 4 * S;
-    static constexpr int NBUF = NBUF_;  // tiles staged: NBUF - 1 ahead of the one computed
-    static constexpr int ACT = NBUF * S6_TILE;
-    static constexpr int CIN = ACT + S6_NB * (NCOL + 1) * S6_QP;
-    static constexpr int DACT = CIN + S6_NB * NCOL * 4 * 16;
-    static constexpr int RED = DACT + S6_NB * NCOL * 4;
+// LDS layout for S sets of 4 columns, NBUF tile buffers and NBW super-blocks per wave. Wave w's
+// activation blocks: qs of column k of its block i at ACT + ((w NBW + i) (NCOL + 1) + k) S6_QP, column
+// NCOL all zeros (the A operand's zero lanes read it); CIN: per block, column k and step j, int4
+// {-32 bsum of group G(j, i), i = 0..3}; DACT: d per block and column; RED: the waves' partial sums of
+// two tiles (float [tile parity][wave][set][64]). With OVERLAY (the operands held in registers, two
+// buffers) the activation blocks live in tile buffer 1, which its first DMA overwrites only after every
+// wave has read them (the first tile's barrier).
+template <int S, int NBUF_, int NBW_> struct S6Layout {
+    static constexpr int NCOL = 4 * S, NBUF = NBUF_, NBW = NBW_, NB = 8 * NBW;
+    static constexpr int ROW_PIECES = NB * Q6K_BYTES / 16;  // 105 NBW
+    static constexpr int PITCH = NBW == 1 ? 107 : 211;      // odd
+    static constexpr int TILE = 16 * PITCH * 16;
+    static constexpr int DMAS = (16 * PITCH + 63) / 64;     // wave-wide DMAs per tile
+    static constexpr int ACT_BYTES = SK_WAVES * NBW * ((NCOL + 1) * S6_QP + NCOL * 64 + NCOL * 4);
+    static constexpr bool OVERLAY = NBW > 1;
+    static constexpr int ACT = OVERLAY ? TILE : NBUF * TILE;
+    static constexpr int CIN = ACT + SK_WAVES * NBW * (NCOL + 1) * S6_QP;
+    static constexpr int DACT = CIN + SK_WAVES * NBW * NCOL * 64;
+    static constexpr int RED = OVERLAY ? NBUF * TILE : DACT + SK_WAVES * NBW * NCOL * 4;
     static constexpr int BYTES = RED + 2 * SK_WAVES * S * 64 * 4;
+    static_assert(ROW_PIECES * 16 == NB * Q6K_BYTES, "whole pieces per row");
+    static_assert(!OVERLAY || (NBUF == 2 && ACT_BYTES <= TILE), "the activations fit the second buffer");
 };
 
-template <int S, int NBUF_>
+template <int S, int NBUF_, int NBW_>
 __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
-    using L = S6Layout<S, NBUF_>;
-    constexpr int NCOL = L::NCOL, NBUF = L::NBUF, AHEAD = NBUF - 1;
+    using L = S6Layout<S, NBUF_, NBW_>;
+    constexpr int NCOL = L::NCOL, NBUF = L::NBUF, AHEAD = NBUF - 1, NBW = L::NBW, NB = L::NB;
+    constexpr int PITCH = L::PITCH, TILE = L::TILE, DMAS = L::DMAS;
+    static_assert(NBW == 1 ? DMAS == 27 : AHEAD == 1, "the wait counts below are written for these");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -216,34 +222,37 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
     if (nt <= 0) return;  // the whole workgroup
 
     // DMA q of a tile (q = wave, wave + 8, ...): lane l fetches the piece for LDS position 64 q + l; the
-    // two pad positions of each row are left alone; the tile's rows are the buffer resource (rows past
-    // the end read as zeros). Every DMA has lanes to fetch (a pad run is 2 positions long).
+    // pad positions of each row are left alone; the tile's rows are the buffer resource (rows past the
+    // end read as zeros). Every DMA has lanes to fetch (a pad run is at most 2 positions long).
     auto dma_tile = [&](int t) {
         const int64_t rt = (tile0 + t) * 16;
         const int64_t rows = min<int64_t>(16, a.nrows - rt);
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(w + rt * a.row_stride), (short)0, (int)(rows * a.row_stride), BUFFER_FLAGS);
-        uint8_t *buf = lds + (t % NBUF) * S6_TILE;
+        uint8_t *buf = lds + (t % NBUF) * TILE;
 #pragma unroll
-        for (int k4 = 0; k4 < (S6_DMAS + SK_WAVES - 1) / SK_WAVES; ++k4) {
+        for (int k4 = 0; k4 < (DMAS + SK_WAVES - 1) / SK_WAVES; ++k4) {
             const int q = wave + SK_WAVES * k4;
-            const int p = 64 * q + lane, rn = p / S6_PITCH, c = p - rn * S6_PITCH;
-            if (q < S6_DMAS && p < 16 * S6_PITCH && c < S6_ROW_PIECES)
+            const int p = 64 * q + lane, rn = p / PITCH, c = p - rn * PITCH;
+            if (q < DMAS && p < 16 * PITCH && c < L::ROW_PIECES)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(buf + 1024 * q),
                                                          16, (uint32_t)(rn * a.row_stride + 16 * c), 0, 0,
                                                          2 /* non-temporal: each weight byte is read once */);
         }
     };
     dma_tile(0);
-    // this wave's DMAs per tile: 4 or 3 (wave-uniform: the waits below are scalar branches)
-    const bool four = (S6_DMAS - __builtin_amdgcn_readfirstlane(wave) + SK_WAVES - 1) / SK_WAVES == 4;
+    // this wave's DMAs per tile (wave-uniform: the waits below are scalar branches)
+    const int ndma = (DMAS - __builtin_amdgcn_readfirstlane(wave) + SK_WAVES - 1) / SK_WAVES;
+    const bool more = ndma == (DMAS + SK_WAVES - 1) / SK_WAVES;
 
-    // this wave's super-block b = wave of every column, staged while the first tile streams in
-    const int b = wave;
-    uint8_t *aq = lds + L::ACT + b * (NCOL + 1) * S6_QP;
-    int *cin = (int *)(lds + L::CIN) + b * NCOL * 16;
-    float *dact = (float *)(lds + L::DACT) + b * NCOL;
-    {
+    // this wave's super-blocks b = wave + 8 i of every column, staged while the first tile streams in
+    uint8_t *aq = lds + L::ACT + wave * NBW * (NCOL + 1) * S6_QP;
+    int *cin = (int *)(lds + L::CIN) + wave * NBW * NCOL * 16;
+    float *dact = (float *)(lds + L::DACT) + wave * NBW * NCOL;
+#pragma unroll
+    for (int bi = 0; bi < NBW; ++bi) {
+        const int b = wave + SK_WAVES * bi;
+        uint8_t *aqb = aq + bi * (NCOL + 1) * S6_QP;
         float v[NCOL][4];
         uint32_t pk[NCOL];
         int bs[NCOL];
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
                     for (int e = 0; e < 4; ++e) v[k][e] = cv ? src[e] : 0.f;
                 }
             } else {
-                const uint8_t *blk = a.q8 + ((int64_t)(blockIdx.y * a.q8_cols + a.col0 + k) * S6_NB + b) * Q8K_BYTES;
+                const uint8_t *blk = a.q8 + ((int64_t)(blockIdx.y * a.q8_cols + a.col0 + k) * NB + b) * Q8K_BYTES;
                 pk[k] = cv ? *(const uint32_t *)(blk + Q8K_QS + 4 * lane) : 0u;
                 bs[k] = cv ? (int)*(const int16_t *)(blk + Q8K_BSUMS + 2 * (lane >> 2)) : 0;
                 dq[k] = cv ? *(const float *)blk : 0.f;
@@ -273,46 +282,53 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
                 const Q8kLane ql = q8k_quantize_lane(v[k]);  // the bytes of ggml's quantize_row_q8_K
                 pk[k] = ql.packed, bs[k] = q8k_quad_sum(ql.sum4), dq[k] = ql.d;
             }
-            *(uint32_t *)(aq + k * S6_QP + 4 * lane) = pk[k];
+            *(uint32_t *)(aqb + k * S6_QP + 4 * lane) = pk[k];
             if ((lane & 3) == 0) {
                 // group G = lane / 4 is output i of step j: G = 8 (i >> 1) + 2 j + (i & 1)
                 const int G = lane >> 2, j = (G >> 1) & 3, i = ((G >> 3) << 1) | (G & 1);
-                cin[(k * 4 + j) * 4 + i] = -32 * bs[k];
+                cin[((bi * NCOL + k) * 4 + j) * 4 + i] = -32 * bs[k];
             }
-            if (lane == 0) dact[k] = dq[k];
+            if (lane == 0) dact[bi * NCOL + k] = dq[k];
         }
-        *(uint32_t *)(aq + NCOL * S6_QP + 4 * lane) = 0u;
+        *(uint32_t *)(aqb + NCOL * S6_QP + 4 * lane) = 0u;
     }
-    // the next tiles only now: the activation loads above were waited for with every older load, so
-    // only tile 0 was in flight with them
-    for (int t = 1; t < AHEAD && t < nt; ++t) dma_tile(t);
+    // the next tiles only now: the activation loads above were waited for, and with them every older
+    // load, so only tile 0 was in flight with them
+    if (!L::OVERLAY)
+        for (int t = 1; t < AHEAD && t < nt; ++t) dma_tile(t);
 
     // the lane's windows in its row (dwords): ql at 64 h + 16 v and 64 h + 32 + 16 v, qh at
-    // 128 + 32 h + 16 v, scales and d at 192; the block starts sh bytes into dword dw0
+    // 128 + 32 h + 16 v, scales and d at 192; block w + 8 i starts sh bytes into dword dw0 + 420 i
     const int h = g >> 1, vv = g & 1;
-    const int dw0 = (Q6K_BYTES * b) >> 2, sh = (Q6K_BYTES * b) & 3;
+    const int dw0 = (Q6K_BYTES * wave) >> 2, sh = (Q6K_BYTES * wave) & 3;
     const int oa = dw0 + 16 * h + 4 * vv, ob = oa + 8, oh = dw0 + 32 + 8 * h + 4 * vv, ot = dw0 + 48;
     // the A operand of set s: column 4 s + n / 4 in lane group n % 4, the zero column elsewhere; the
-    // accumulator's start (-32 bsums) of the lane's column g. Both stay in registers for every tile.
+    // accumulator's start (-32 bsums) of the lane's column g. Held in registers for every tile up to 16
+    // (block, column) pairs.
 #ifndef TQ_S6_HOLD_MAX
 #define TQ_S6_HOLD_MAX 4
 #endif
-    constexpr bool HOLD = S <= TQ_S6_HOLD_MAX;
+    constexpr bool HOLD = S * NBW <= TQ_S6_HOLD_MAX;
+    static_assert(HOLD || !L::OVERLAY, "the overlaid activations are read once");
     const bool aon = (n & 3) == g;
     const int abase = 128 * h + 16 * vv;
-    auto a_op = [&](int s, int j) {
-        return *(const v4i *)(aq + (aon ? 4 * s + (n >> 2) : NCOL) * S6_QP + abase + 32 * j);
+    auto a_op = [&](int bi, int s, int j) {
+        return *(const v4i *)(aq + (bi * (NCOL + 1) + (aon ? 4 * s + (n >> 2) : NCOL)) * S6_QP + abase + 32 * j);
     };
     // (read as v4i: an int4 read here made the compiler wait for every DMA in flight)
-    auto c_op = [&](int s, int j) { return *(const v4i *)((const uint8_t *)cin + (4 * s + g) * 64 + 16 * j); };
-    v4i Ah[HOLD ? S : 1][4], Ch[HOLD ? S : 1][4];
-    float dh[HOLD ? S : 1];
+    auto c_op = [&](int bi, int s, int j) {
+        return *(const v4i *)((const uint8_t *)cin + ((bi * NCOL + 4 * s + g) * 4 + j) * 16);
+    };
+    constexpr int NH = HOLD ? NBW * S : 1;
+    v4i Ah[NH][4], Ch[NH][4];
+    float dh[NH];
     if (HOLD) {
 #pragma unroll
-        for (int s = 0; s < (HOLD ? S : 1); ++s) {
+        for (int x = 0; x < NH; ++x) {
+            const int bi = x / S, s = x % S;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) Ah[s][j] = a_op(s, j), Ch[s][j] = c_op(s, j);
-            dh[s] = dact[4 * s + g];
+            for (int j = 0; j < 4; ++j) Ah[x][j] = a_op(bi, s, j), Ch[x][j] = c_op(bi, s, j);
+            dh[x] = dact[bi * NCOL + 4 * s + g];
         }
     }
     float *red = (float *)(lds + L::RED);
@@ -338,89 +354,109 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
         // (stores issued between them are older than the last DMAs and are waited for too)
         const int later = min(AHEAD - 1, nt - 1 - t);
         if (later == 0) __builtin_amdgcn_s_waitcnt(0 | 0x0F70);
-        else if (later == 1) { if (four) __builtin_amdgcn_s_waitcnt(4 | 0x0F70); else __builtin_amdgcn_s_waitcnt(3 | 0x0F70); }
-        else { if (four) __builtin_amdgcn_s_waitcnt(8 | 0x0F70); else __builtin_amdgcn_s_waitcnt(6 | 0x0F70); }
+        else if (later == 1) { if (more) __builtin_amdgcn_s_waitcnt(4 | 0x0F70); else __builtin_amdgcn_s_waitcnt(3 | 0x0F70); }
+        else { if (more) __builtin_amdgcn_s_waitcnt(8 | 0x0F70); else __builtin_amdgcn_s_waitcnt(6 | 0x0F70); }
         lds_barrier();  // every wave's DMAs of tile t have landed; every wave is done with tile t - 1
         if (t > 0) store_tile(t - 1);
         // tile t + AHEAD goes into the buffer of tile t - 1
         if (t + AHEAD < nt) dma_tile(t + AHEAD);
-        const uint32_t *row = (const uint32_t *)(lds + (t % NBUF) * S6_TILE + 16 * S6_PITCH * n);
-        uint32_t ra[5], rb[5], rh[5], rt[5];
+        float acc[S];
 #pragma unroll
-        for (int i = 0; i < 5; ++i) ra[i] = row[oa + i], rb[i] = row[ob + i], rh[i] = row[oh + i], rt[i] = row[ot + i];
-        uint32_t A[4], B[4], H[4], T[5];
+        for (int s = 0; s < S; ++s) acc[s] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            A[i] = align_bytes(ra[i + 1], ra[i], sh);
-            B[i] = align_bytes(rb[i + 1], rb[i], sh);
-            H[i] = align_bytes(rh[i + 1], rh[i], sh);
-            T[i] = align_bytes(rt[i + 1], rt[i], sh);
-        }
-        T[4] = align_bytes(rt[4], rt[4], sh);  // d in the low half (the byte after it is not used)
-        const float dw = half_bits_to_float(T[4]);
-        // codes of the lane's four groups 8 h + 2 j + v, one plane per step j (q - 32 via the accumulator)
-        const uint32_t m4 = 0x0f0f0f0fu;
-        v4i P[4];
+        for (int bi = 0; bi < NBW; ++bi) {
+            const uint32_t *row = (const uint32_t *)(lds + (t % NBUF) * TILE + 16 * PITCH * n) + 420 * bi;
+            uint32_t ra[5], rb[5], rh[5], rt[5];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t Hl = H[i] & 0x33333333u, Hh = (H[i] >> 2) & 0x33333333u;
-            P[0][i] = (int)bfi(m4, A[i], Hl << 4);
-            P[1][i] = (int)bfi(m4, B[i], Hh << 4);
-            P[2][i] = (int)bfi(m4, A[i] >> 4, Hl);
-            P[3][i] = (int)bfi(m4, B[i] >> 4, Hh);
+            for (int i = 0; i < 5; ++i) ra[i] = row[oa + i], rb[i] = row[ob + i], rh[i] = row[oh + i], rt[i] = row[ot + i];
+            uint32_t A[4], B[4], H[4], T[5];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                A[i] = align_bytes(ra[i + 1], ra[i], sh);
+                B[i] = align_bytes(rb[i + 1], rb[i], sh);
+                H[i] = align_bytes(rh[i + 1], rh[i], sh);
+                T[i] = align_bytes(rt[i + 1], rt[i], sh);
+            }
+            T[4] = align_bytes(rt[4], rt[4], sh);  // d in the low half (the byte after it is not used)
+            const float dw = half_bits_to_float(T[4]);
+            // codes of the lane's four groups 8 h + 2 j + v, one plane per step j (q - 32 via the accumulator)
+            const uint32_t m4 = 0x0f0f0f0fu;
+            v4i P[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t Hl = H[i] & 0x33333333u, Hh = (H[i] >> 2) & 0x33333333u;
+                P[0][i] = (int)bfi(m4, A[i], Hl << 4);
+                P[1][i] = (int)bfi(m4, B[i], Hh << 4);
+                P[2][i] = (int)bfi(m4, A[i] >> 4, Hl);
+                P[3][i] = (int)bfi(m4, B[i] >> 4, Hh);
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int x = HOLD ? bi * S + s : 0;
+                int isum = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4i R = __builtin_amdgcn_mfma_i32_16x16x64_i8(HOLD ? Ah[x][j] : a_op(bi, s, j), P[j],
+                                                                        HOLD ? Ch[x][j] : c_op(bi, s, j), 0, 0, 0);
+                    // scales of groups 2 j, 2 j + 1 (bytes of T[j / 2]) and 8 + 2 j, 9 + 2 j (of T[2 + j / 2])
+                    const int bp = 16 * (j & 1);
+                    isum = mad24(sext8(T[j >> 1], bp), R[0], isum);
+                    isum = mad24(sext8(T[j >> 1], bp + 8), R[1], isum);
+                    isum = mad24(sext8(T[2 + (j >> 1)], bp), R[2], isum);
+                    isum = mad24(sext8(T[2 + (j >> 1)], bp + 8), R[3], isum);
+                }
+                acc[s] += (dw * (HOLD ? dh[x] : dact[bi * NCOL + 4 * s + g])) * (float)isum;
+            }
         }
         float *rw = red + (t & 1) * SK_WAVES * S * 64;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            int isum = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const v4i R = __builtin_amdgcn_mfma_i32_16x16x64_i8(HOLD ? Ah[HOLD ? s : 0][j] : a_op(s, j), P[j],
-                                                                    HOLD ? Ch[HOLD ? s : 0][j] : c_op(s, j), 0, 0, 0);
-                // scales of groups 2 j, 2 j + 1 (bytes of T[j / 2]) and 8 + 2 j, 9 + 2 j (of T[2 + j / 2])
-                const int bp = 16 * (j & 1);
-                isum = mad24(sext8(T[j >> 1], bp), R[0], isum);
-                isum = mad24(sext8(T[j >> 1], bp + 8), R[1], isum);
-                isum = mad24(sext8(T[2 + (j >> 1)], bp), R[2], isum);
-                isum = mad24(sext8(T[2 + (j >> 1)], bp + 8), R[3], isum);
-            }
-            rw[(wave * S + s) * 64 + lane] = (dw * (HOLD ? dh[HOLD ? s : 0] : dact[4 * s + g])) * (float)isum;
-        }
+        for (int s = 0; s < S; ++s) rw[(wave * S + s) * 64 + lane] = acc[s];
     }
     lds_barrier();
     store_tile(nt - 1);
 }
 
 bool skinny_q6k_supported(const GemvArgs &a) {
-    return a.nb == S6_NB && a.row_stride % 16 == 0 && (uintptr_t)a.w % 16 == 0 && a.w_s2 % 16 == 0 &&
+    return (a.nb == 8 || a.nb == 16) && a.row_stride % 16 == 0 && (uintptr_t)a.w % 16 == 0 && a.w_s2 % 16 == 0 &&
            a.w_s3 % 16 == 0 && 16 * a.row_stride < (1ll << 31);
 }
 
-// Tile buffers and workgroups per CU of the Q6_K kernel: up to 4 columns two workgroups of two buffers
-// each, more columns one workgroup of 4 (up to 8 columns) or 3 buffers (LDS-bound).
+int skinny_q6k_cols_per_launch(int nb) { return nb == 8 ? 16 : 8; }
+
+// Tile buffers and workgroups per CU of the Q6_K kernel. K = 2048: up to 4 columns two workgroups of
+// two buffers each, more columns one workgroup of 4 (up to 8 columns) or 3 buffers (LDS-bound).
+// K = 4096: one workgroup of two buffers, the activations staged in the second (up to 8 columns).
 #ifndef TQ_S6_NARROW
 #define TQ_S6_NARROW 2
 #endif
-template <int S, int NBUF>
+template <int S, int NBUF, int NBW>
 static void launch_s6(const GemvArgs &a, int64_t ntiles, int per_cu, hipStream_t stream) {
     const unsigned gx = (unsigned)std::min<int64_t>(ntiles, (int64_t)device_cu_count() * per_cu);
-    k_skinny_q6k<S, NBUF><<<dim3(gx, (unsigned)a.nbatch), SK_WAVES * 64, S6Layout<S, NBUF>::BYTES, stream>>>(a);
+    k_skinny_q6k<S, NBUF, NBW>
+        <<<dim3(gx, (unsigned)a.nbatch), SK_WAVES * 64, S6Layout<S, NBUF, NBW>::BYTES, stream>>>(a);
 }
 
 hipError_t launch_skinny_q6k(const GemvArgs &a, hipStream_t stream) {
-    if (!skinny_q6k_supported(a) || a.ncols < 1 || a.ncols > 16) return hipErrorNotSupported;
+    if (!skinny_q6k_supported(a) || a.ncols < 1 || a.ncols > skinny_q6k_cols_per_launch(a.nb))
+        return hipErrorNotSupported;
     const int64_t ntiles = (a.nrows + 15) / 16;
-    switch ((a.ncols + 3) / 4) {
+    const int sets = (a.ncols + 3) / 4;
+    if (a.nb == 16) {
+        if (sets == 1) launch_s6<1, 2, 2>(a, ntiles, 1, stream);
+        else launch_s6<2, 2, 2>(a, ntiles, 1, stream);
+        return hipGetLastError();
+    }
+    switch (sets) {
 #if TQ_S6_NARROW == 2
-    case 1: launch_s6<1, 2>(a, ntiles, 2, stream); break;
+    case 1: launch_s6<1, 2, 1>(a, ntiles, 2, stream); break;
 #elif TQ_S6_NARROW == 3
-    case 1: launch_s6<1, 3>(a, ntiles, 1, stream); break;
+    case 1: launch_s6<1, 3, 1>(a, ntiles, 1, stream); break;
 #else
-    case 1: launch_s6<1, 4>(a, ntiles, 1, stream); break;
+    case 1: launch_s6<1, 4, 1>(a, ntiles, 1, stream); break;
 #endif
-    case 2: launch_s6<2, 4>(a, ntiles, 1, stream); break;
-    case 3: launch_s6<3, 3>(a, ntiles, 1, stream); break;
-    default: launch_s6<4, 3>(a, ntiles, 1, stream); break;
+    case 2: launch_s6<2, 4, 1>(a, ntiles, 1, stream); break;
+    case 3: launch_s6<3, 3, 1>(a, ntiles, 1, stream); break;
+    default: launch_s6<4, 3, 1>(a, ntiles, 1, stream); break;
     }
     return hipGetLastError();
 }
