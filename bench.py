@@ -626,10 +626,10 @@ def bench_prefill(ggml, torch, dev, only=False):
 def bench_secondary(ggml, torch, dev):
     res = {}
     # the Q6_K output head 151936 x 2048 (255 MB, two copies alternated) at batch 1 and 4: the whole
-    # MUL_MAT (F32 activations) and the GEMV kernel alone on Q8_K activations, mean per launch over
-    # 400 back-to-back launches; the Q4_K GEMV at the same bandwidth-bound size (175 MB) at batch 1
+    # MUL_MAT (F32 activations) and the kernel alone on Q8_K activations, mean per launch over 400
+    # back-to-back launches; Q4_K at the same bandwidth-bound size (175 MB) at batch 1 and 4
     for label, tyb, k, n, m in (("q6_K", ggml.Type.Q6_K, 2048, 151936, 1), ("q6_K", ggml.Type.Q6_K, 2048, 151936, 4),
-                                ("q4_K", ggml.Type.Q4_K, 2048, 151936, 1)):
+                                ("q4_K", ggml.Type.Q4_K, 2048, 151936, 1), ("q4_K", ggml.Type.Q4_K, 2048, 151936, 4)):
         W = make_weights(ggml, torch, tyb, k, n, 2, seed=5 + m, dev=dev)
         x = torch.randn((m, k), device=dev)
         out = torch.empty((m, n), device=dev)

@@ -295,3 +295,41 @@ def test_q6_K_k4096_batched_decode_shapes(gpu, n, m):
     want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
     check(y, want, f"q6_K k={k} n={n} m={m}")
     assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("k,n,m,q8", [(2048, 4101, 5, False), (4096, 8200, 20, False), (2048, 20000, 64, False),
+                                      (4096, 4096, 4, True), (2048, 20000, 3, False), (4096, 16400, 4, False)])
+def test_q4_K_persistent_skinny_shapes(gpu, k, n, m, q8):
+    """Q4_K at K = 2048 / 4096 with 256 and more row tiles runs the persistent skinny kernel (tiles
+    streamed two at a time per workgroup, activation operands held in registers): a partial last tile,
+    two super-blocks per wave with two column tiles, four column tiles, Q8_K columns given as such, and
+    3 / 4 F32 columns on matrices of 16K rows and more (smaller ones keep those on the GEMV)."""
+    _case(f"q4_K persistent skinny k={k} n={n} m={m} q8={q8}")
+    ty = TYPES["q4_K"]
+    w = make_weights(ty, k, n, 1, seed=k + 3 * n + m, device=gpu)
+    x = normal((m, k), 13 * m + n)
+    xt = torch.from_numpy(x).to(gpu)
+    if q8:
+        xt = ggml.QTensor(ggml.Type.Q8_K, (k, m), ggml.quantize_q8_K(xt).view(-1))
+    y = ggml.mul_mat(w, xt).cpu().numpy().reshape(m, n)
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
+    check(y, want, f"q4_K k={k} n={n} m={m}")
+    assert np.all(np.isfinite(y))
+
+
+def test_q4_K_persistent_skinny_broadcast(gpu):
+    """The persistent Q4_K kernel over batches: a [2048, 4100, 2] broadcast over b [2048, 9, 4], b rows
+    strided, dst a strided view whose padding must stay untouched."""
+    _case("q4_K persistent skinny broadcast")
+    ty = TYPES["q4_K"]
+    k, n, m = 2048, 4100, 9
+    w = make_weights(ty, k, n, 2, seed=21, device=gpu)
+    xb = normal((4, m, k + 64), 22)
+    xt = torch.from_numpy(xb).to(gpu)[:, :, 32:32 + k]
+    out_big = torch.full((4, m, n + 8), float("nan"), device=gpu)
+    out = out_big[:, :, :n]
+    ggml.mul_mat(w, xt, out=out)
+    got = out_big.cpu().numpy()
+    assert np.all(np.isnan(got[:, :, n:])), "wrote outside dst"
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, np.ascontiguousarray(xb[:, :, 32:32 + k]), ne2=2)
+    check(got[:, :, :n], want, "q4_K persistent skinny broadcast")

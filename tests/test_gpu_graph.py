@@ -46,12 +46,12 @@ def _check_replays(op, outs, noise):
 @pytest.mark.parametrize("tname,k,n,m", [("q6_K", 2048, 20000, 1), ("q4_K", 2048, 4096, 2), ("q4_K", 4096, 300, 4),
                                          ("q6_K", 2048, 1000, 6), ("q6_K", 2048, 1000, 12), ("q6_K", 4096, 700, 5),
                                          ("q6_K", 512, 300, 6),
-                                         ("q4_K", 2048, 4096, 16)])
+                                         ("q4_K", 2048, 4096, 16), ("q4_K", 2048, 8192, 24)])
 def test_mul_mat_decode_in_graph(gpu, tname, k, n, m):
     """Decode MUL_MAT: the LDS-streamed GEMV (batch 1..4), the register GEMV (Q6_K at K = 512, 6
     columns), the Q6_K MFMA kernel (K = 2048: 6 columns quantized inside it, 12 with the Q8_K pass in the
-    workspace; K = 4096, 5 columns) and the skinny Q4_K MFMA kernel (16 columns, with the Q8_K pass in the
-    workspace)."""
+    workspace; K = 4096, 5 columns) and the skinny Q4_K MFMA kernels (16 and 24 columns, the second
+    persistent, with the Q8_K pass in the workspace)."""
     _case(f"mul_mat {tname} k={k} n={n} m={m}")
     ty = ggml.Type.Q4_K if tname == "q4_K" else ggml.Type.Q6_K
     w = make_weights(ty, k, n, 1, seed=k + n + m, device=gpu)

@@ -212,9 +212,21 @@ constexpr int64_t SKINNY_MIN_COLS = 4, SKINNY_MAX_COLS = 64;
 static bool skinny_columns(int type, int64_t ncols) {
     return ncols >= SKINNY_MIN_COLS && ncols <= SKINNY_MAX_COLS && skinny_supported(type, ncols);
 }
-static bool use_skinny(int type, int64_t ncols, int nb, bool f32) {
+// Q4_K matrices of 16K rows and more that the persistent skinny kernel takes (K = 2048 or 4096,
+// contiguous 16-byte aligned rows): its stream beats the GEMV from 3 columns (151936 x 2048, F32 columns
+// in graphs: 3 / 4 columns 50.0 / 50.7 us on the GEMV, 41.7 at 4 on the skinny kernel with its Q8_K
+// pass; at 4096 and 12288 rows the GEMV stays ahead at 4 columns: 6.71 / 9.54 against 6.80 / 10.17 us).
+constexpr int64_t SKINNY_BIG_ROWS = 16384;
+static bool skinny_big(const tq_tensor *a) {
+    const int64_t nb = a->ne[0] / QK;
+    return a->type == TQ_TYPE_Q4_K && (nb == 8 || nb == 16) && a->ne[1] >= SKINNY_BIG_ROWS &&
+           (int64_t)a->nb[1] == nb * Q4K_BYTES && (uintptr_t)a->data % 16 == 0 && a->nb[2] % 16 == 0 &&
+           a->nb[3] % 16 == 0;
+}
+static bool use_skinny(const tq_tensor *a, int64_t ncols, int nb, bool f32) {
+    if (skinny_big(a) && ncols >= 3 && ncols <= 4) return true;
     if (f32 && ncols <= 4 && ncols * nb <= 32) return false;
-    return skinny_columns(type, ncols);
+    return skinny_columns(a->type, ncols);
 }
 
 // Q6_K at K = 2048 or 4096 from 3 to 32 columns (2 on matrices of 64K rows and more): the Q6_K MFMA
@@ -257,7 +269,7 @@ static bool use_mmq(const tq_tensor *a, int64_t ncols) {
 // quantization launch of its own on MI355X); the Q6_K MFMA kernel quantizes up to 8 columns itself.
 static bool quantize_in_workgroup(const tq_tensor *a, int64_t ncols, int nb) {
     if (use_skinny6(a, ncols)) return ncols <= SKINNY6_QUANT_MAX_COLS;
-    return !use_mmq(a, ncols) && !use_skinny(a->type, ncols, nb, true) && ncols * nb <= 32;
+    return !use_mmq(a, ncols) && !use_skinny(a, ncols, nb, true) && ncols * nb <= 32;
 }
 
 static size_t q8_bytes(const tq_tensor *b) { return align_up(row_size(TQ_TYPE_Q8_K, b->ne[0]) * (size_t)nrows(b), 256); }
@@ -365,7 +377,7 @@ static int check_mul_mat(const tq_tensor *a, const tq_tensor *b, const tq_tensor
     if (b->ne[2] * b->ne[3] > 65535) return fail(TQ_STATUS_FAILED, "more than 65535 batch matrices");
     const int nb = (int)(a->ne[0] / QK);
     const bool mmq = use_mmq(a, b->ne[1]);
-    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32) || use_skinny6(a, b->ne[1]);
+    const bool skinny = use_skinny(a, b->ne[1], nb, b->type == TQ_TYPE_F32) || use_skinny6(a, b->ne[1]);
     const int nc_max = nb ? (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb)) : 8;
     if (!mmq && !skinny && nc_max < 1) return fail(TQ_STATUS_FAILED, "K = %lld is above the GEMV limit", (long long)a->ne[0]);
     if (mmq && b->ne[1] > 0x7fffffff) return fail(TQ_STATUS_FAILED, "more than 2^31 - 1 columns");
@@ -380,7 +392,7 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
     const int nb = (int)(a->ne[0] / QK);
     const bool pre_quantized = b->type == TQ_TYPE_Q8_K;
     const bool mmq = use_mmq(a, b->ne[1]);
-    const bool skinny = use_skinny(a->type, b->ne[1], nb, b->type == TQ_TYPE_F32);
+    const bool skinny = use_skinny(a, b->ne[1], nb, b->type == TQ_TYPE_F32);
     const bool skinny6 = use_skinny6(a, b->ne[1]);
     const int nc_max = (int)std::min<size_t>(8, gemv_max_lds() / (gemv_lds_per_col_block() * nb));
 

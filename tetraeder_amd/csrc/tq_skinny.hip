@@ -461,10 +461,168 @@ hipError_t launch_skinny_q6k(const GemvArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------------
+// Q4_K at K = 2048 or 4096, persistent: the one-workgroup-per-tile kernel above waits for each tile's
+// DMAs with nothing else in flight (a 151936 x 2048 matrix at 4 columns ran at 26% of HBM). Here a few
+// workgroups per CU each run over a contiguous range of 16-row tiles, two tile buffers each (the next
+// tile's DMAs in flight while one is computed), wave w owns super-blocks w + 8 i (i < NBW = K / 2048) of
+// every tile and holds its activation operands for them in registers for the whole range, and the
+// waves' partial sums of a tile are added up after the next tile's barrier (one barrier per tile).
+// Rows are staged at an odd pitch of 9 nb + 1 pieces (the same piece of 16 rows on 16 bank groups).
+// ------------------------------------------------------------------------------------------------
+template <int MT, int NBW_> struct S4Layout {
+    static constexpr int NBW = NBW_, NB = 8 * NBW;
+    static constexpr int ROW_PIECES = NB * Q4K_BYTES / 16;  // 72 NBW
+    static constexpr int PITCH = ROW_PIECES + 1;            // odd
+    static constexpr int TILE = 16 * PITCH * 16;
+    static constexpr int DMAS = (16 * PITCH + 63) / 64;
+    static constexpr int RED = 2 * TILE;                     // v4f [tile parity][wave][column tile][64]
+    static constexpr int BYTES = RED + 2 * SK_WAVES * MT * 64 * 16;
+};
+
+template <int MT, int NBW_>
+__global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_p(SkinnyArgs a) {
+    using L = S4Layout<MT, NBW_>;
+    constexpr int NBW = L::NBW, NB = L::NB, PITCH = L::PITCH, TILE = L::TILE, DMAS = L::DMAS;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
+    const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
+    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * a.ncols * NB * Q8K_BYTES;
+    float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
+    const int ncols = a.ncols;  // 1 .. 16 MT
+    const int64_t ntiles = (a.nrows + 15) / 16;
+    const int64_t tile0 = ntiles * blockIdx.x / gridDim.x;
+    const int nt = (int)(ntiles * (blockIdx.x + 1) / gridDim.x - tile0);
+    if (nt <= 0) return;  // the whole workgroup
+
+    // the activation operands of this wave's super-blocks, loaded ahead of the first DMAs (their wait
+    // then waits for nothing else)
+    const int ntile = (ncols + 15) >> 4;  // column tiles with a valid column
+    Q4kTileAct act[NBW][MT];
+#pragma unroll
+    for (int bi = 0; bi < NBW; ++bi)
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct)
+            if (ct < ntile)
+                load_tile_act(act[bi][ct], 16 * ct, ncols, [&](int k) {
+                    return q8 + ((int64_t)k * NB + wave + SK_WAVES * bi) * Q8K_BYTES;
+                });
+
+    // DMA q of a tile (q = wave, wave + 8, ...): lane l fetches the piece for LDS position 64 q + l; the
+    // pad position of each row is left alone; the tile's rows are the buffer resource (rows past the end
+    // read as zeros)
+    auto dma_tile = [&](int t) {
+        const int64_t rt = (tile0 + t) * 16;
+        const int64_t rows = min<int64_t>(16, a.nrows - rt);
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(w + rt * a.row_stride), (short)0, (int)(rows * a.row_stride), BUFFER_FLAGS);
+        uint8_t *buf = lds + (t & 1) * TILE;
+#pragma unroll
+        for (int k4 = 0; k4 < (DMAS + SK_WAVES - 1) / SK_WAVES; ++k4) {
+            const int q = wave + SK_WAVES * k4;
+            const int p = 64 * q + lane, rn = p / PITCH, c = p - rn * PITCH;
+            if (q < DMAS && p < 16 * PITCH && c < L::ROW_PIECES)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(buf + 1024 * q),
+                                                         16, (uint32_t)(rn * a.row_stride + 16 * c), 0, 0,
+                                                         2 /* non-temporal: each weight byte is read once */);
+        }
+    };
+    dma_tile(0);
+    v4f *red = (v4f *)(lds + L::RED);
+
+    // adds up the waves' partial sums of tile t (in red[t % 2]) and stores them: element x of the tile
+    // (row x % 16 fastest, so 16 lanes store 16 consecutive floats of a column)
+    auto store_tile = [&](int t) {
+        const v4f *rp = red + (t & 1) * SK_WAVES * MT * 64;
+        for (int x = threadIdx.x; x < ntile * 256; x += SK_WAVES * 64) {
+            const int nn = x & 15, i4 = (x >> 4) & 3, gg = (x >> 6) & 3, ct = x >> 8;
+            float sum = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < SK_WAVES; ++w2) sum += rp[(w2 * MT + ct) * 64 + nn + 16 * gg][i4];
+            const int col = 16 * ct + 4 * gg + i4;
+            const int64_t r = (tile0 + t) * 16 + nn;
+            if (col < ncols && r < a.nrows) dst[col * a.d_s1 + r] = sum;
+        }
+    };
+
+    for (int t = 0; t < nt; ++t) {
+        __builtin_amdgcn_s_waitcnt(0 | 0x0F70);  // this wave's DMAs of tile t (the only ones in flight)
+        lds_barrier();  // every wave's DMAs of tile t have landed; every wave is done with tile t - 1
+        if (t > 0) store_tile(t - 1);
+        if (t + 1 < nt) dma_tile(t + 1);  // into the buffer of tile t - 1
+        const uint8_t *rowp = lds + (t & 1) * TILE + 16 * PITCH * n;
+        const bool rv = (tile0 + t) * 16 + n < a.nrows;
+        v4f acc[MT];
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct) acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int bi = 0; bi < NBW; ++bi) {
+            const int cb = 9 * (wave + SK_WAVES * bi);  // the block's first piece in its row
+            Q4kLaneBlock wl;
+            wl.hdr = *(const uint4 *)(rowp + 16 * cb);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) wl.qw[s4] = *(const uint4 *)(rowp + 16 * (cb + 1 + 2 * s4 + (g & 1)));
+            Q4kPlanes P;
+            q4k_planes(wl, rv, P);
+#pragma unroll
+            for (int ct = 0; ct < MT; ++ct)
+                if (ct < ntile) q4k_tile_mma(P, act[bi][ct], acc[ct]);
+        }
+        v4f *rw = red + (t & 1) * SK_WAVES * MT * 64;
+#pragma unroll
+        for (int ct = 0; ct < MT; ++ct)
+            if (ct < ntile) rw[(wave * MT + ct) * 64 + lane] = acc[ct];
+    }
+    lds_barrier();
+    store_tile(nt - 1);
+}
+
+// The persistent Q4_K kernel takes K = 2048 with up to 64 columns and K = 4096 with up to 32 (its
+// activation operands stay in registers), contiguous 16-byte aligned matrices.
+static bool skinny_q4k_p_supported(const SkinnyArgs &a) {
+    return (a.nb == 8 || (a.nb == 16 && a.ncols <= 32)) && a.row_stride == (int64_t)a.nb * Q4K_BYTES &&
+           (uintptr_t)a.w % 16 == 0 && a.w_s2 % 16 == 0 && a.w_s3 % 16 == 0 && 16 * a.row_stride < (1ll << 31);
+}
+
+template <int MT, int NBW>
+static void launch_s4(const SkinnyArgs &a, int per_cu, hipStream_t stream) {
+    const int64_t ntiles = (a.nrows + 15) / 16;
+    const unsigned gx = (unsigned)std::min<int64_t>(ntiles, (int64_t)device_cu_count() * per_cu);
+    k_skinny_q4k_p<MT, NBW><<<dim3(gx, (unsigned)a.nbatch), SK_WAVES * 64, S4Layout<MT, NBW>::BYTES, stream>>>(a);
+}
+
+// Row tiles from which the persistent kernel is taken (below it every tile has a workgroup of its own
+// and the kernel above starts all of them at once). On MI355X, Q8_K columns, persistent against one
+// workgroup per tile: 151936 x 2048 at 4 / 8 / 16 / 32 / 64 columns 42.3 / 40.8 / 44.4 / 58.0 / 110.5 us
+// against 82.5 / 84.1 / 90.1 / 197.8 / 303.5; 151936 x 4096 at 4 / 16 / 32: 95.1 / 94.5 / 127.4 against
+// 121.9 / 148.3 / 316.1; 12288 x 4096 at 8 / 16 / 32: 12.1 / 12.8 / 17.2 against 12.8 / 14.3 / 26.7;
+// 4096 x 2048 (256 tiles) at 8 / 16 / 32: 4.64 / 4.80 / 6.61 against 4.77 / 5.05 / 6.71; 2048 x 4096
+// (128 tiles) at 8: 6.07 against 5.97.
+#ifndef TQ_S4P_MIN_TILES
+#define TQ_S4P_MIN_TILES 256
+#endif
+
 bool skinny_supported(int type, int64_t ncols) { return type == FMT_Q4K && ncols >= 1 && ncols <= 0x7fffffff; }
 
 hipError_t launch_skinny(int type, const SkinnyArgs &a, hipStream_t stream) {
     if (!skinny_supported(type, a.ncols)) return hipErrorNotSupported;
+    if ((a.nrows + 15) / 16 >= TQ_S4P_MIN_TILES && skinny_q4k_p_supported(a)) {
+        const int mt = (a.ncols + 15) / 16;
+        if (a.nb == 8) {
+            switch (mt) {
+            case 1: launch_s4<1, 1>(a, 2, stream); break;
+            case 2: launch_s4<2, 1>(a, 2, stream); break;
+            case 3: launch_s4<3, 1>(a, 1, stream); break;
+            default: launch_s4<4, 1>(a, 1, stream); break;
+            }
+        } else {
+            if (mt == 1) launch_s4<1, 2>(a, 1, stream);
+            else launch_s4<2, 2>(a, 1, stream);
+        }
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((a.nrows + 15) / 16), (unsigned)a.nbatch);
     const int mt = (a.ncols + 15) / 16;
     if (a.nb <= SK_LDS_NB_MAX && (int64_t)16 * a.row_stride < (1ll << 31)) {
