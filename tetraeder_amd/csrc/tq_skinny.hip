@@ -470,20 +470,41 @@ hipError_t launch_skinny_q6k(const GemvArgs &a, hipStream_t stream) {
 // waves' partial sums of a tile are added up after the next tile's barrier (one barrier per tile).
 // Rows are staged at an odd pitch of 9 nb + 1 pieces (the same piece of 16 rows on 16 bank groups).
 // ------------------------------------------------------------------------------------------------
-template <int MT, int NBW_> struct S4Layout {
-    static constexpr int NBW = NBW_, NB = 8 * NBW;
+template <int MT, int NBW_, int NBUF_> struct S4Layout {
+    static constexpr int NBW = NBW_, NB = 8 * NBW, NBUF = NBUF_;
     static constexpr int ROW_PIECES = NB * Q4K_BYTES / 16;  // 72 NBW
     static constexpr int PITCH = ROW_PIECES + 1;            // odd
     static constexpr int TILE = 16 * PITCH * 16;
     static constexpr int DMAS = (16 * PITCH + 63) / 64;
-    static constexpr int RED = 2 * TILE;                     // v4f [tile parity][wave][column tile][64]
+    static constexpr int RED = NBUF * TILE;                  // v4f [tile parity][wave][column tile][64]
     static constexpr int BYTES = RED + 2 * SK_WAVES * MT * 64 * 16;
 };
 
-template <int MT, int NBW_>
-__global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_p(SkinnyArgs a) {
-    using L = S4Layout<MT, NBW_>;
+// Waits until at most n of this wave's vector memory operations are outstanding (n wave-uniform, < 16).
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0 | 0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(1 | 0x0F70); break;
+    case 2: __builtin_amdgcn_s_waitcnt(2 | 0x0F70); break;
+    case 3: __builtin_amdgcn_s_waitcnt(3 | 0x0F70); break;
+    case 4: __builtin_amdgcn_s_waitcnt(4 | 0x0F70); break;
+    case 5: __builtin_amdgcn_s_waitcnt(5 | 0x0F70); break;
+    case 6: __builtin_amdgcn_s_waitcnt(6 | 0x0F70); break;
+    case 7: __builtin_amdgcn_s_waitcnt(7 | 0x0F70); break;
+    case 8: __builtin_amdgcn_s_waitcnt(8 | 0x0F70); break;
+    case 9: __builtin_amdgcn_s_waitcnt(9 | 0x0F70); break;
+    case 10: __builtin_amdgcn_s_waitcnt(10 | 0x0F70); break;
+    default: __builtin_amdgcn_s_waitcnt(0 | 0x0F70); break;  // (never above 10 here) the strictest
+    }
+}
+
+template <int MT, int NBW_, int NBUF_, int WPC>
+__global__ __launch_bounds__(SK_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2 * WPC)))
+void k_skinny_q4k_p(SkinnyArgs a) {
+    using L = S4Layout<MT, NBW_, NBUF_>;
     constexpr int NBW = L::NBW, NB = L::NB, PITCH = L::PITCH, TILE = L::TILE, DMAS = L::DMAS;
+    constexpr int NBUF = L::NBUF, AHEAD = NBUF - 1;
+    static_assert((AHEAD - 1) * ((DMAS + SK_WAVES - 1) / SK_WAVES) <= 10, "wait_vm's range");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -518,7 +539,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_p(SkinnyArgs a) {
         const int64_t rows = min<int64_t>(16, a.nrows - rt);
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(w + rt * a.row_stride), (short)0, (int)(rows * a.row_stride), BUFFER_FLAGS);
-        uint8_t *buf = lds + (t & 1) * TILE;
+        uint8_t *buf = lds + (t % NBUF) * TILE;
 #pragma unroll
         for (int k4 = 0; k4 < (DMAS + SK_WAVES - 1) / SK_WAVES; ++k4) {
             const int q = wave + SK_WAVES * k4;
@@ -529,7 +550,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_p(SkinnyArgs a) {
                                                          2 /* non-temporal: each weight byte is read once */);
         }
     };
-    dma_tile(0);
+    for (int t = 0; t < AHEAD && t < nt; ++t) dma_tile(t);
+    // this wave's DMAs per tile (wave-uniform)
+    const int ndma = (DMAS - __builtin_amdgcn_readfirstlane(wave) + SK_WAVES - 1) / SK_WAVES;
     v4f *red = (v4f *)(lds + L::RED);
 
     // adds up the waves' partial sums of tile t (in red[t % 2]) and stores them: element x of the tile
@@ -548,11 +571,13 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_p(SkinnyArgs a) {
     };
 
     for (int t = 0; t < nt; ++t) {
-        __builtin_amdgcn_s_waitcnt(0 | 0x0F70);  // this wave's DMAs of tile t (the only ones in flight)
+        // this wave's DMAs of tile t are done once at most those of the tiles after it are outstanding
+        // (stores issued between them are older than the last DMAs and are waited for too)
+        wait_vm(min(AHEAD - 1, nt - 1 - t) * ndma);
         lds_barrier();  // every wave's DMAs of tile t have landed; every wave is done with tile t - 1
         if (t > 0) store_tile(t - 1);
-        if (t + 1 < nt) dma_tile(t + 1);  // into the buffer of tile t - 1
-        const uint8_t *rowp = lds + (t & 1) * TILE + 16 * PITCH * n;
+        if (t + AHEAD < nt) dma_tile(t + AHEAD);  // into the buffer of tile t - 1
+        const uint8_t *rowp = lds + (t % NBUF) * TILE + 16 * PITCH * n;
         const bool rv = (tile0 + t) * 16 + n < a.nrows;
         v4f acc[MT];
 #pragma unroll
@@ -586,11 +611,12 @@ static bool skinny_q4k_p_supported(const SkinnyArgs &a) {
            (uintptr_t)a.w % 16 == 0 && a.w_s2 % 16 == 0 && a.w_s3 % 16 == 0 && 16 * a.row_stride < (1ll << 31);
 }
 
-template <int MT, int NBW>
-static void launch_s4(const SkinnyArgs &a, int per_cu, hipStream_t stream) {
+template <int MT, int NBW, int NBUF, int WPC>
+static void launch_s4(const SkinnyArgs &a, hipStream_t stream) {
     const int64_t ntiles = (a.nrows + 15) / 16;
-    const unsigned gx = (unsigned)std::min<int64_t>(ntiles, (int64_t)device_cu_count() * per_cu);
-    k_skinny_q4k_p<MT, NBW><<<dim3(gx, (unsigned)a.nbatch), SK_WAVES * 64, S4Layout<MT, NBW>::BYTES, stream>>>(a);
+    const unsigned gx = (unsigned)std::min<int64_t>(ntiles, (int64_t)device_cu_count() * WPC);
+    k_skinny_q4k_p<MT, NBW, NBUF, WPC>
+        <<<dim3(gx, (unsigned)a.nbatch), SK_WAVES * 64, S4Layout<MT, NBW, NBUF>::BYTES, stream>>>(a);
 }
 
 // Row tiles from which the persistent kernel is taken (below it every tile has a workgroup of its own
@@ -610,16 +636,23 @@ hipError_t launch_skinny(int type, const SkinnyArgs &a, hipStream_t stream) {
     if (!skinny_supported(type, a.ncols)) return hipErrorNotSupported;
     if ((a.nrows + 15) / 16 >= TQ_S4P_MIN_TILES && skinny_q4k_p_supported(a)) {
         const int mt = (a.ncols + 15) / 16;
+        // two buffers: three (two tiles ahead) measured slower (151936 x 2048 at 32 columns 59.7 ->
+        // 83.4 us at one workgroup per CU, at 64 columns 110.5 -> 119.5, K = 4096 95.1 -> 98.5)
+        // (three workgroups per CU at one column tile, 80 VGPRs with a few spilled, were no faster on
+        // 151936 x 2048 and slower on 12288 x 2048: 8.40 against 8.02 us at 4 columns)
+#ifndef TQ_S4P_WPC1
+#define TQ_S4P_WPC1 2
+#endif
         if (a.nb == 8) {
             switch (mt) {
-            case 1: launch_s4<1, 1>(a, 2, stream); break;
-            case 2: launch_s4<2, 1>(a, 2, stream); break;
-            case 3: launch_s4<3, 1>(a, 1, stream); break;
-            default: launch_s4<4, 1>(a, 1, stream); break;
+            case 1: launch_s4<1, 1, 2, TQ_S4P_WPC1>(a, stream); break;
+            case 2: launch_s4<2, 1, 2, 2>(a, stream); break;
+            case 3: launch_s4<3, 1, 2, 1>(a, stream); break;
+            default: launch_s4<4, 1, 2, 1>(a, stream); break;
             }
         } else {
-            if (mt == 1) launch_s4<1, 2>(a, 1, stream);
-            else launch_s4<2, 2>(a, 1, stream);
+            if (mt == 1) launch_s4<1, 2, 2, 1>(a, stream);
+            else launch_s4<2, 2, 2, 1>(a, stream);
         }
         return hipGetLastError();
     }
