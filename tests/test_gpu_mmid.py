@@ -186,7 +186,7 @@ def test_mul_mat_id_prefill_routings(gpu, case):
     32 experts (32 tokens each: one 32-column chunk, activations staged in LDS; at K = 4096 the chunk does
     not fit the LDS and the waves read the activations themselves), on 16 experts (64 tokens each: one
     64-column chunk), on 8 experts (128 each: two chunks), 90% -1 (a few tokens on most experts); and a
-    Q6_K matrix (the GEMV path), all against the oracle."""
+    Q6_K matrix (the grouped Q6_K MFMA kernel, 16-column chunks at K = 2048), all against the oracle."""
     _case(case)
     ty = ggml.Type.Q6_K if case.startswith("q6_K") else ggml.Type.Q4_K
     k = 4096 if "_K4096" in case else 2048
@@ -201,6 +201,30 @@ def test_mul_mat_id_prefill_routings(gpu, case):
         ids[rng.random(ids.shape) < 0.9] = -1
     w = make_experts(ty, k, n, E, seed=T + 5, device=gpu)
     b = normal((T, 1, k), T + 6)
+    out = torch.full((T, used, n), 5.0, device=gpu)
+    ggml.mul_mat_id(w, torch.from_numpy(b).to(gpu), torch.from_numpy(ids).to(gpu), out=out)
+    want = O.mul_mat_id(ty.id, w.data.cpu().numpy(), k, n, E, b, ids)
+    check(out.cpu().numpy(), want, ids, case)
+
+
+@pytest.mark.parametrize("case", ["uniform_T128", "uniform_T512", "skew16_T256", "neg90_T512"])
+def test_mul_mat_id_q6_K_down_prefill(gpu, case):
+    """The Qwen3-30B-A3B down projections at prefill size (Q6_K 768 -> 2048, 128 experts, top-8, one
+    activation row per slot) on the grouped Q6_K MFMA kernel: about 8 and 32 tokens per expert (one 16- or
+    32-column chunk), 128 tokens on each of 16 experts (four 32-column chunks), 90% -1."""
+    _case(f"q6_K down {case}")
+    ty = ggml.Type.Q6_K
+    k, n, E, used = 768, 2048, 128, 8
+    T = int(case.split("_T")[1])
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    ids = np.zeros((T, used), dtype=np.int32)
+    for t in range(T):
+        pool = 16 if case.startswith("skew16") else E
+        ids[t] = rng.permutation(pool)[:used]
+    if case.startswith("neg90"):
+        ids[rng.random(ids.shape) < 0.9] = -1
+    w = make_experts(ty, k, n, E, seed=T + 15, device=gpu)
+    b = normal((T, used, k), T + 16)
     out = torch.full((T, used, n), 5.0, device=gpu)
     ggml.mul_mat_id(w, torch.from_numpy(b).to(gpu), torch.from_numpy(ids).to(gpu), out=out)
     want = O.mul_mat_id(ty.id, w.data.cpu().numpy(), k, n, E, b, ids)

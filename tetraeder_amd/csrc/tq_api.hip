@@ -560,7 +560,7 @@ int tq_mul_mat_id(const tq_tensor *as, const tq_tensor *b, const tq_tensor *ids,
     m.d_s1 = (int64_t)(dst->nb[1] / 4);
     m.d_s2 = (int64_t)(dst->nb[2] / 4);
     m.route = ws ? (int32_t *)(ws + q8_bytes(b)) : nullptr;
-    m.chunk = mmid_mfma_chunk(as->type, m.n_expert, n_used * T);
+    m.chunk = mmid_mfma_chunk(as->type, m.n_expert, n_used * T, m.nb);
     m.q8_bytes = (int64_t)row_size(TQ_TYPE_Q8_K, b->ne[0]) * b->ne[1] * b->ne[2];
     if (n_used * T <= mmid_small_max_slots()) {
         // decode: one launch, routing resolved per workgroup, activations quantized in LDS

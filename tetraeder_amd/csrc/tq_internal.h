@@ -134,7 +134,7 @@ struct MmidArgs {
 size_t mmid_route_bytes(int n_expert, int64_t n_slots);
 hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream);
 // Columns per work item of the grouped int8-MFMA MUL_MAT_ID for these operands (0: the GEMV kernel)
-int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots);
+int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots, int nb);
 // decode-size routing (n_used * T <= 256): one launch, F32 activations quantized in each workgroup
 constexpr int64_t mmid_small_max_slots() { return 256; }
 hipError_t launch_mul_mat_id_small(int type, const MmidArgs &a, const float *b, int64_t b_s1, int64_t b_s2, int b_vec,

@@ -386,6 +386,141 @@ void k_mmid_mfma_q4k(MmidArgs a) {
     mmid_mfma_q4k<MT, false>(a, nullptr);
 }
 
+// Q6_K experts with several tokens each (the Qwen3 down projections at prefill): the same work items,
+// a wave per 16-row tile of the expert over all its super-blocks, the chunk's columns in sets of 4 on
+// the Q6_K MFMA step of tq_skinny.h (4 columns x 4 scale groups per 16x16x64 step). The chunk's
+// activation blocks are staged once per workgroup in the step's operand layout (qs at a 272-byte
+// pitch with a zero column for the A operand's masked lanes, -32 x bsums per step, d); the weights come
+// straight from memory, each 16-byte window realigned from aligned dwords (Q6_K blocks are 2-byte
+// aligned), the first super-blocks' loads in flight while the chunk is staged.
+constexpr int MMID_Q6_QP = 272;
+__host__ __device__ static size_t mmid_q6k_lds(int nb, int ncol) {
+    return (size_t)nb * ((ncol + 1) * MMID_Q6_QP + ncol * 64 + ncol * 4);
+}
+constexpr size_t MMID_Q6_LDS_MAX = 64 * 1024;  // two workgroups per CU
+
+// The windows of one Q6_K super-block for lane group g = 2h + v (5 aligned dwords each), read straight
+// from memory: the block at blk (2-byte aligned) starts sh bytes into the first dword of each. The fifth
+// tail dword is needed only at sh = 2 (its last bytes are then the block's d); at sh = 0 the fourth is
+// read again, so no load passes the block's end. d is read on its own.
+struct Q6kWin {
+    uint32_t a[5], b[5], h[5], t[5], sh;
+    uint32_t dbits;
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, int g) {
+        const int hh = g >> 1, vv = g & 1;
+        sh = (uint32_t)((uintptr_t)blk & 3u);
+        const uint32_t *base = (const uint32_t *)(blk - sh);
+        const int oa = 16 * hh + 4 * vv, ob = oa + 8, oh = 32 + 8 * hh + 4 * vv;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) a[i] = base[oa + i], b[i] = base[ob + i], h[i] = base[oh + i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] = base[48 + i];
+        t[4] = base[sh ? 52 : 51];
+        dbits = *(const uint16_t *)(blk + 208);
+    }
+};
+
+template <int S>
+__global__ __launch_bounds__(MMID_SK_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void k_mmid_mfma_q6k(MmidArgs a) {
+    constexpr int NCOL = 4 * S;
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int64_t col_q8[NCOL], col_dst[NCOL];  // a column's Q8_K row (bytes) and dst row (floats)
+    const int item = blockIdx.y;
+    const int n_slots = a.n_used * a.ntok;
+    const int n_items = a.route[2];
+    const int32_t *rec = a.route + mmid_items_offset(a.n_expert, n_slots) + (int64_t)item * (4 + NCOL);
+    const int4 hdr = *(const int4 *)rec;
+    const int my_slot = (int)threadIdx.x < NCOL ? rec[4 + threadIdx.x] : 0;
+    if (item >= n_items) return;  // fewer work items than grid rows: the whole workgroup leaves
+    const int e = hdr.x, nvalid = hdr.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int nb = a.nb;
+    const int64_t row = (int64_t)blockIdx.x * MMID_SK_ROWS + 16 * wave + n;
+    const bool rv = row < a.nrows;
+    const uint8_t *wrow = a.w + (int64_t)e * a.w_s2 + (rv ? row : 0) * a.w_s1;
+    // the first two super-blocks' windows are in flight while the chunk is staged
+    Q6kWin win[2];
+    win[0].load(wrow, g);
+    win[1].load(wrow + (int64_t)min(1, nb - 1) * Q6K_BYTES, g);
+    if ((int)threadIdx.x < nvalid) {
+        const int s = my_slot, j = s % a.n_used, t = s / a.n_used;
+        col_q8[threadIdx.x] = ((int64_t)t * a.ne11 + j % a.ne11) * nb * Q8K_BYTES;
+        col_dst[threadIdx.x] = j * a.d_s1 + t * a.d_s2;
+    }
+    lds_barrier();  // the weight loads stay in flight
+    // the chunk's blocks (b, k), one wave each: qs at act + (b (NCOL + 1) + k) 272, column NCOL zero;
+    // columns past nvalid are zero
+    uint8_t *act = lds;
+    int *cin = (int *)(lds + (size_t)nb * (NCOL + 1) * MMID_Q6_QP);
+    float *dact = (float *)((uint8_t *)cin + (size_t)nb * NCOL * 64);
+    // BATCH blocks per wave at a time: their loads are all issued before the first is written
+    constexpr int BATCH = 8;
+    const int nblk = nb * (NCOL + 1);
+    for (int p0 = wave; p0 < nblk; p0 += BATCH * MMID_SK_WAVES) {
+        uint32_t pk[BATCH];
+        int bs[BATCH];
+        float dq[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+            const int p = p0 + i * MMID_SK_WAVES, b = p / (NCOL + 1), k = p - b * (NCOL + 1);
+            pk[i] = 0u, bs[i] = 0, dq[i] = 0.f;
+            if (p < nblk && k < nvalid) {
+                const uint8_t *blk = a.q8 + col_q8[k] + (int64_t)b * Q8K_BYTES;
+                pk[i] = *(const uint32_t *)(blk + Q8K_QS + 4 * lane);
+                bs[i] = (int)*(const int16_t *)(blk + Q8K_BSUMS + 2 * (lane >> 2));
+                dq[i] = *(const float *)blk;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+            const int p = p0 + i * MMID_SK_WAVES, b = p / (NCOL + 1), k = p - b * (NCOL + 1);
+            if (p >= nblk) break;
+            if (k < NCOL)
+                q6k_stage_column(pk[i], bs[i], dq[i], act + (b * (NCOL + 1) + k) * MMID_Q6_QP, cin + (b * NCOL + k) * 16,
+                                 dact + b * NCOL + k);
+            else *(uint32_t *)(act + (b * (NCOL + 1) + k) * MMID_Q6_QP + 4 * lane) = 0u;
+        }
+    }
+    lds_barrier();
+    const int nset = (nvalid + 3) >> 2;  // sets with a valid column (the rest are skipped)
+    const bool aon = (n & 3) == g;
+    const int abase = 128 * (g >> 1) + 16 * (g & 1);
+    float acc[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[s] = 0.f;
+    // super-block b from window set b % 2, which then loads block b + 2 (clamped: the last blocks load
+    // the final one again, from the cache)
+    auto step = [&](Q6kWin &wn, int b) {
+        v4i P[4];
+        uint32_t T[4];
+        q6k_planes(wn.a, wn.b, wn.h, wn.t, wn.sh, P, T);
+        const float dw = rv ? half_bits_to_float(wn.dbits) : 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (s < nset) {
+                const uint8_t *ap = act + (b * (NCOL + 1) + (aon ? 4 * s + (n >> 2) : NCOL)) * MMID_Q6_QP + abase;
+                const uint8_t *cp = (const uint8_t *)cin + (b * NCOL + 4 * s + g) * 64;
+                const int isum = q6k_set_isum(P, T, [&](int j) { return *(const v4i *)(ap + 32 * j); },
+                                              [&](int j) { return *(const v4i *)(cp + 16 * j); });
+                acc[s] += (dw * dact[b * NCOL + 4 * s + g]) * (float)isum;
+            }
+        }
+        wn.load(wrow + (int64_t)min(b + 2, nb - 1) * Q6K_BYTES, g);
+    };
+    for (int b = 0; b < nb; b += 2) {
+        step(win[0], b);
+        if (b + 1 < nb) step(win[1], b + 1);
+    }
+    if (rv) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k = 4 * s + g;
+            if (k < nvalid) a.dst[col_dst[k] + row] = acc[s];
+        }
+    }
+}
+
 // The same work split over K instead of rows, for K = 2048 (8 super-blocks, one per wave): wave w owns
 // super-block w of all 8 row tiles of the workgroup and keeps the chunk's activation operands for it in
 // registers. The row tiles (16 rows x 1152 bytes, contiguous in the expert) come into LDS by wave-wide
@@ -811,10 +946,16 @@ static hipError_t launch_fmt(const MmidArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots) {
-    if (type != FMT_Q4K || n_slots <= 0) return 0;
+int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots, int nb) {
+    if ((type != FMT_Q4K && type != FMT_Q6K) || n_slots <= 0) return 0;
     const double per_expert = (double)n_slots / (double)std::min<int64_t>(n_expert, n_slots);
     if (per_expert < MMID_MFMA_MIN_COLS) return 0;
+    if (type == FMT_Q6K) {
+        // chunks of up to 32 columns whose staged blocks leave room for two workgroups per CU
+        const int ch = per_expert <= 16 ? 16 : 32;
+        if (mmid_q6k_lds(nb, ch) <= MMID_Q6_LDS_MAX) return ch;
+        return mmid_q6k_lds(nb, 16) <= MMID_Q6_LDS_MAX ? 16 : 0;
+    }
     return per_expert <= 16 ? 16 : per_expert <= 32 ? 32 : 64;
 }
 
@@ -831,6 +972,12 @@ hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream) {
     if (a.chunk > 0) {
         const dim3 grid((unsigned)((a.nrows + MMID_SK_ROWS - 1) / MMID_SK_ROWS),
                         (unsigned)mmid_max_items(a.n_expert, n_slots, a.chunk));
+        if (type == FMT_Q6K) {
+            const size_t lds = mmid_q6k_lds(a.nb, a.chunk);
+            if (a.chunk == 16) k_mmid_mfma_q6k<4><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            else k_mmid_mfma_q6k<8><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            return hipGetLastError();
+        }
         const int mt = a.chunk / 16;
         // the staged activation chunk must fit the LDS next to the kernel's own arrays (and its offsets
         // the 32-bit range of a buffer resource)

@@ -160,4 +160,64 @@ __device__ __forceinline__ void q4k_skinny_step(const uint8_t *__restrict__ wb, 
     for (int ct = 0; ct < MT; ++ct) q4k_tile_mma(P, t[ct], acc[ct]);
 }
 
+// ---- Q6_K: 4 activation columns x 4 scale groups per 16x16x64 step ----
+// ggml's vec_dot_q6_K_q8_K per super-block: d * d_y * sum_G sc_G * sum_{k in G} (q_k - 32) y_k over 16
+// groups of 16 weights with signed 8-bit scales. In step j (of 4) lane group g = 2h + v holds, for its
+// weight row, the 16 codes of group G(j, g) = 8h + 2j + v; A-operand row 4c + i holds column c's Q8_K
+// bytes of group G(j, i) in the k-slots of lane group i and zeros elsewhere; the accumulator starts
+// from -32 times the column's bsums of those groups. Lane l of the result then holds the four group sums
+// of step j for weight row l % 16 and column l / 16.
+
+// The code planes of a Q6_K block for lane group g = 2h + v from 5 aligned dwords of each of its windows
+// (ql at 64h + 16v and 64h + 32 + 16v, qh at 128 + 32h + 16v, the scales at 192), the block starting sh
+// bytes into each window's first dword: P[j] = the 16 codes (0..63) of group 8h + 2j + v, T = the 16
+// scale bytes. (6-bit codes: the low nibble from ql, bits 4-5 from the qh field of the quarter; a
+// bit-field insert merges them without the neighbour byte's bits leaking in.)
+__device__ __forceinline__ void q6k_planes(const uint32_t (&ra)[5], const uint32_t (&rb)[5], const uint32_t (&rh)[5],
+                                           const uint32_t (&rt)[5], uint32_t sh, v4i (&P)[4], uint32_t (&T)[4]) {
+    const uint32_t m4 = 0x0f0f0f0fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t A = align_bytes(ra[i + 1], ra[i], sh), B = align_bytes(rb[i + 1], rb[i], sh);
+        const uint32_t H = align_bytes(rh[i + 1], rh[i], sh);
+        T[i] = align_bytes(rt[i + 1], rt[i], sh);
+        const uint32_t Hl = H & 0x33333333u, Hh = (H >> 2) & 0x33333333u;
+        P[0][i] = (int)bfi(m4, A, Hl << 4);
+        P[1][i] = (int)bfi(m4, B, Hh << 4);
+        P[2][i] = (int)bfi(m4, A >> 4, Hl);
+        P[3][i] = (int)bfi(m4, B >> 4, Hh);
+    }
+}
+
+// sum_G sc_G * (the group sums of one set of 4 columns) over the 4 steps of a super-block: a_op(j) and
+// c_op(j) give the A operand and the accumulator start of step j.
+template <class AOp, class COp>
+__device__ __forceinline__ int q6k_set_isum(const v4i (&P)[4], const uint32_t (&T)[4], AOp a_op, COp c_op) {
+    int isum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const v4i R = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_op(j), P[j], c_op(j), 0, 0, 0);
+        // scales of groups 2j, 2j + 1 (bytes of T[j / 2]) and 8 + 2j, 9 + 2j (of T[2 + j / 2])
+        const int bp = 16 * (j & 1);
+        isum = mad24(sext8(T[j >> 1], bp), R[0], isum);
+        isum = mad24(sext8(T[j >> 1], bp + 8), R[1], isum);
+        isum = mad24(sext8(T[2 + (j >> 1)], bp), R[2], isum);
+        isum = mad24(sext8(T[2 + (j >> 1)], bp + 8), R[3], isum);
+    }
+    return isum;
+}
+
+// Stages super-block b of a column into the Q6_K operand layout (called by one wave; lane l has the
+// column's packed qs bytes 4l .. 4l + 3 in pk, its quad's bsum (group l / 4) in bs and d in dq): qs at
+// aq (256 bytes), -32 x bsum of group G at cin[j * 4 + i] for G = 8 (i >> 1) + 2 j + (i & 1), d at *dp.
+__device__ __forceinline__ void q6k_stage_column(uint32_t pk, int bs, float dq, uint8_t *aq, int *cin, float *dp) {
+    const int lane = (int)(threadIdx.x & 63);
+    *(uint32_t *)(aq + 4 * lane) = pk;
+    if ((lane & 3) == 0) {
+        const int G = lane >> 2, j = (G >> 1) & 3, i = ((G >> 3) << 1) | (G & 1);
+        cin[j * 4 + i] = -32 * bs;
+    }
+    if (lane == 0) *dp = dq;
+}
+
 }  // namespace tq

@@ -282,13 +282,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
                 const Q8kLane ql = q8k_quantize_lane(v[k]);  // the bytes of ggml's quantize_row_q8_K
                 pk[k] = ql.packed, bs[k] = q8k_quad_sum(ql.sum4), dq[k] = ql.d;
             }
-            *(uint32_t *)(aqb + k * S6_QP + 4 * lane) = pk[k];
-            if ((lane & 3) == 0) {
-                // group G = lane / 4 is output i of step j: G = 8 (i >> 1) + 2 j + (i & 1)
-                const int G = lane >> 2, j = (G >> 1) & 3, i = ((G >> 3) << 1) | (G & 1);
-                cin[((bi * NCOL + k) * 4 + j) * 4 + i] = -32 * bs[k];
-            }
-            if (lane == 0) dact[bi * NCOL + k] = dq[k];
+            q6k_stage_column(pk[k], bs[k], dq[k], aqb + k * S6_QP, cin + (bi * NCOL + k) * 16, dact + bi * NCOL + k);
         }
         *(uint32_t *)(aqb + NCOL * S6_QP + 4 * lane) = 0u;
     }
@@ -369,42 +363,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q6k(GemvArgs a) {
             uint32_t ra[5], rb[5], rh[5], rt[5];
 #pragma unroll
             for (int i = 0; i < 5; ++i) ra[i] = row[oa + i], rb[i] = row[ob + i], rh[i] = row[oh + i], rt[i] = row[ot + i];
-            uint32_t A[4], B[4], H[4], T[5];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                A[i] = align_bytes(ra[i + 1], ra[i], sh);
-                B[i] = align_bytes(rb[i + 1], rb[i], sh);
-                H[i] = align_bytes(rh[i + 1], rh[i], sh);
-                T[i] = align_bytes(rt[i + 1], rt[i], sh);
-            }
-            T[4] = align_bytes(rt[4], rt[4], sh);  // d in the low half (the byte after it is not used)
-            const float dw = half_bits_to_float(T[4]);
+            // d in the low half of the fifth tail dword once realigned (the byte after it is not used)
+            const float dw = half_bits_to_float(align_bytes(rt[4], rt[4], sh));
             // codes of the lane's four groups 8 h + 2 j + v, one plane per step j (q - 32 via the accumulator)
-            const uint32_t m4 = 0x0f0f0f0fu;
             v4i P[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t Hl = H[i] & 0x33333333u, Hh = (H[i] >> 2) & 0x33333333u;
-                P[0][i] = (int)bfi(m4, A[i], Hl << 4);
-                P[1][i] = (int)bfi(m4, B[i], Hh << 4);
-                P[2][i] = (int)bfi(m4, A[i] >> 4, Hl);
-                P[3][i] = (int)bfi(m4, B[i] >> 4, Hh);
-            }
+            uint32_t T[4];
+            q6k_planes(ra, rb, rh, rt, sh, P, T);
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 const int x = HOLD ? bi * S + s : 0;
-                int isum = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const v4i R = __builtin_amdgcn_mfma_i32_16x16x64_i8(HOLD ? Ah[x][j] : a_op(bi, s, j), P[j],
-                                                                        HOLD ? Ch[x][j] : c_op(bi, s, j), 0, 0, 0);
-                    // scales of groups 2 j, 2 j + 1 (bytes of T[j / 2]) and 8 + 2 j, 9 + 2 j (of T[2 + j / 2])
-                    const int bp = 16 * (j & 1);
-                    isum = mad24(sext8(T[j >> 1], bp), R[0], isum);
-                    isum = mad24(sext8(T[j >> 1], bp + 8), R[1], isum);
-                    isum = mad24(sext8(T[2 + (j >> 1)], bp), R[2], isum);
-                    isum = mad24(sext8(T[2 + (j >> 1)], bp + 8), R[3], isum);
-                }
+                const int isum = q6k_set_isum(P, T, [&](int j) { return HOLD ? Ah[x][j] : a_op(bi, s, j); },
+                                              [&](int j) { return HOLD ? Ch[x][j] : c_op(bi, s, j); });
                 acc[s] += (dw * (HOLD ? dh[x] : dact[bi * NCOL + 4 * s + g])) * (float)isum;
             }
         }
