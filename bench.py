@@ -678,6 +678,22 @@ def bench_secondary(ggml, torch, dev):
         log(f"mul_mat_id T={T}: {res[f'mul_mat_id_q4_K_2048x768x128_T{T}']}")
     del w
     torch.cuda.empty_cache()
+    # and the down projections: Q6_K [768 -> 2048] x 128 experts, one activation row per slot
+    k, n = 768, 2048
+    w = make_weights(ggml, torch, ggml.Type.Q6_K, k, n * E, 1, seed=4, dev=dev)[0]
+    w = ggml.QTensor(w.type, (k, n, E), w.data)
+    for T in (512, 2048):
+        ids = torch.from_numpy(moe_ids(np, T, seed=T)).to(dev)
+        x = torch.randn((T, 8, k), device=dev)
+        out = torch.empty((T, 8, n), device=dev)
+        ws = torch.empty(max(1, ggml.mul_mat_id_workspace_size(w, x, ids)), dtype=torch.uint8, device=dev)
+        us = time_graph(torch, lambda i: ggml.mul_mat_id(w, x, ids, out=out, workspace=ws), 4)
+        valid = int((ids >= 0).sum().item())
+        key = f"mul_mat_id_q6_K_768x2048x128_T{T}"
+        res[key] = {"op_us": round(us, 1), "int_TOPS": round(2 * valid * n * k / us / 1e6, 1)}
+        log(f"mul_mat_id down T={T}: {res[key]}")
+    del w
+    torch.cuda.empty_cache()
     return res
 
 
