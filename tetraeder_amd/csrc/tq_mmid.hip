@@ -397,7 +397,7 @@ constexpr int MMID_Q6_QP = 272;
 __host__ __device__ static size_t mmid_q6k_lds(int nb, int ncol) {
     return (size_t)nb * ((ncol + 1) * MMID_Q6_QP + ncol * 64 + ncol * 4);
 }
-constexpr size_t MMID_Q6_LDS_MAX = 64 * 1024;  // two workgroups per CU
+constexpr size_t MMID_Q6_LDS_MAX = 78 * 1024;  // two workgroups per CU
 
 // The windows of one Q6_K super-block for lane group g = 2h + v (5 aligned dwords each), read straight
 // from memory: the block at blk (2-byte aligned) starts sh bytes into the first dword of each. The fifth
@@ -951,10 +951,12 @@ int mmid_mfma_chunk(int type, int n_expert, int64_t n_slots, int nb) {
     const double per_expert = (double)n_slots / (double)std::min<int64_t>(n_expert, n_slots);
     if (per_expert < MMID_MFMA_MIN_COLS) return 0;
     if (type == FMT_Q6K) {
-        // chunks of up to 32 columns whose staged blocks leave room for two workgroups per CU
-        const int ch = per_expert <= 16 ? 16 : 32;
-        if (mmid_q6k_lds(nb, ch) <= MMID_Q6_LDS_MAX) return ch;
-        return mmid_q6k_lds(nb, 16) <= MMID_Q6_LDS_MAX ? 16 : 0;
+        // the widest chunk whose staged blocks leave room for two workgroups per CU: 64 columns only
+        // above 48 tokens per expert (Qwen3 down at 2048 tokens 376 -> 344 us; at 512, about 29 tokens per
+        // expert, 32-column chunks are faster: 132 against 138 us)
+        for (int ch = per_expert <= 16 ? 16 : per_expert <= 48 ? 32 : 64; ch >= 16; ch /= 2)
+            if (mmid_q6k_lds(nb, ch) <= MMID_Q6_LDS_MAX) return ch;
+        return 0;
     }
     return per_expert <= 16 ? 16 : per_expert <= 32 ? 32 : 64;
 }
@@ -975,7 +977,8 @@ hipError_t launch_mul_mat_id(int type, const MmidArgs &a, hipStream_t stream) {
         if (type == FMT_Q6K) {
             const size_t lds = mmid_q6k_lds(a.nb, a.chunk);
             if (a.chunk == 16) k_mmid_mfma_q6k<4><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
-            else k_mmid_mfma_q6k<8><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            else if (a.chunk == 32) k_mmid_mfma_q6k<8><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
+            else k_mmid_mfma_q6k<16><<<grid, MMID_SK_WAVES * 64, lds, stream>>>(a);
             return hipGetLastError();
         }
         const int mt = a.chunk / 16;
