@@ -14,11 +14,12 @@
 //                 grid.x splits an expert's rows; each workgroup stages its expert's columns (the
 //                 tokens routed to it, up to 8 at a time) in LDS and streams the expert's weights once
 //                 for all of them with the GEMV core;
-//   or, Q4_K experts with several tokens each (prefill), the grouped int8-MFMA kernels over the work
-//                 items (a chunk of up to 16 MT columns of one routed expert): grid.y walks the items,
-//                 grid.x the expert's 128-row tiles; k_mmid_ksplit_q4k at K = 2048 (the super-blocks
+//   or, experts with several tokens each (prefill), the grouped int8-MFMA kernels over the work items
+//                 (a chunk of 16, 32 or 64 columns of one routed expert): grid.y walks the items, grid.x
+//                 the expert's 128-row tiles; for Q4_K k_mmid_ksplit_q4k at K = 2048 (the super-blocks
 //                 split over the waves, weight tiles staged by LDS DMA), k_mmid_mfma_q4k(_lds)
-//                 otherwise (a wave per 16-row tile), both on the skinny step of tq_skinny.h.
+//                 otherwise (a wave per 16-row tile), for Q6_K k_mmid_mfma_q6k (a wave per 16-row tile),
+//                 all on the skinny steps of tq_skinny.h.
 #include "tq_gemv_core.h"
 #include "tq_internal.h"
 #include "tq_skinny.h"
