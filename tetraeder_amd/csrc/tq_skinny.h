@@ -1,5 +1,6 @@
-// tq_skinny.h -- one super-block step of the Q4_K int8-MFMA kernels for a few activation columns (the
-// skinny MUL_MAT of tq_skinny.hip and the grouped MUL_MAT_ID of tq_mmid.hip).
+// tq_skinny.h -- one super-block step of the Q4_K and Q6_K int8-MFMA kernels for a few activation
+// columns (the skinny MUL_MAT of tq_skinny.hip and the grouped MUL_MAT_ID of tq_mmid.hip); the Q6_K
+// step is at the end.
 //
 // ggml's dot product per Q4_K super-block (vec_dot_q4_K_q8_K):
 //   d_y * (d * sum_j sc_j * sum_{k in j} q_k y_k  -  dmin * sum_j m_j * S_j),  S_j = sum_{k in j} y_k
