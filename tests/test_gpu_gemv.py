@@ -226,12 +226,12 @@ def test_q4_K_batched_decode_shapes(gpu, k, n, m):
 
 
 @pytest.mark.parametrize("n,m", [(17, 3), (17, 4), (300, 7), (4101, 13), (2048, 16), (5000, 20), (1000, 32), (1000, 33),
-                                 (512, 64)])
+                                 (4101, 48), (512, 64), (700, 65), (300, 100)])
 def test_q6_K_batched_decode_shapes(gpu, n, m):
-    """Q6_K at K = 2048 with 3..32 columns runs the Q6_K MFMA kernel (16 columns per launch, up to 8 of
-    them quantized inside it), from 33 the prefill kernel: row counts that are no multiple of the 16-row
-    tiles, fewer tiles than workgroups and several tiles per workgroup, column counts that are no
-    multiple of 4."""
+    """Q6_K at K = 2048 with 3..64 columns (below 64K rows) runs the Q6_K MFMA kernel (16 columns per
+    launch, up to 8 of them quantized inside it), from 65 the prefill kernel: row counts that are no
+    multiple of the 16-row tiles, fewer tiles than workgroups and several tiles per workgroup, column
+    counts that are no multiple of 4."""
     _case(f"q6_K skinny n={n} m={m}")
     ty = TYPES["q6_K"]
     k = 2048
@@ -282,10 +282,11 @@ def test_q6_K_skinny_dynamic_range_and_zero_columns(gpu, m):
             check(y[i], want[i], f"q6_K column {i}")
 
 
-@pytest.mark.parametrize("n,m", [(17, 3), (300, 4), (4101, 8), (1000, 13), (2048, 32), (1000, 2)])
+@pytest.mark.parametrize("n,m", [(17, 3), (300, 4), (4101, 8), (1000, 13), (2048, 32), (1000, 2), (700, 48), (700, 49)])
 def test_q6_K_k4096_batched_decode_shapes(gpu, n, m):
     """Q6_K at K = 4096: the Q6_K MFMA kernel with two super-blocks per wave (8 columns per launch, the
-    activations staged in the second tile buffer), and the GEMV at 2 columns on a small matrix."""
+    activations staged in the second tile buffer) up to 48 columns, the prefill kernel from 49, and the
+    GEMV at 2 columns on a small matrix."""
     _case(f"q6_K k=4096 n={n} m={m}")
     ty = TYPES["q6_K"]
     k = 4096
@@ -314,6 +315,23 @@ def test_q4_K_persistent_skinny_shapes(gpu, k, n, m, q8):
     y = ggml.mul_mat(w, xt).cpu().numpy().reshape(m, n)
     want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x)[0]
     check(y, want, f"q4_K k={k} n={n} m={m}")
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("k,n,m,ne2", [(2048, 4100, 65, 1), (4096, 4096, 128, 1), (2048, 1000, 96, 1),
+                                       (2048, 4100, 100, 2), (2048, 4096, 129, 1)])
+def test_q4_K_wide_skinny_shapes(gpu, k, n, m, ne2):
+    """Q4_K below 16K rows with 65..128 columns runs the skinny kernels in 64-column launches, each on
+    its part of the Q8_K columns (129 columns go to the prefill kernel): a partial last launch, the
+    persistent and the per-tile kernel (1000 rows: fewer than 256 tiles), and batches of b broadcast
+    over a [k, n, 1] matrix, so the batch stride of the Q8_K columns is the full column count."""
+    _case(f"q4_K wide skinny k={k} n={n} m={m} ne2={ne2}")
+    ty = TYPES["q4_K"]
+    w = make_weights(ty, k, n, 1, seed=k + n + 5 * m, device=gpu)
+    x = normal((ne2, m, k), 17 * m + n)
+    y = ggml.mul_mat(w, torch.from_numpy(x).to(gpu)).cpu().numpy().reshape(ne2, m, n)
+    want = O.mul_mat(ty.id, w.data.cpu().numpy(), k, n, x, ne2=1).reshape(ne2, m, n)
+    check(y, want, f"q4_K wide skinny k={k} n={n} m={m} ne2={ne2}")
     assert np.all(np.isfinite(y))
 
 

@@ -223,15 +223,27 @@ static bool skinny_big(const tq_tensor *a) {
            (int64_t)a->nb[1] == nb * Q4K_BYTES && (uintptr_t)a->data % 16 == 0 && a->nb[2] % 16 == 0 &&
            a->nb[3] % 16 == 0;
 }
+// Below 16K rows the skinny Q4_K kernel also takes 65..128 columns, 64 per launch: the prefill kernel
+// is far slower there up to 128 (2048 x 4096 at 65 / 128 columns 16.2 / 21.3 us, 34.0 / 35.5 at 65 / 96
+// on the prefill kernel, which takes 129 in 32.7; 2048 x 12288 at 128 / 129 33.0 / 38.9).
+constexpr int64_t SKINNY_WIDE_MAX_COLS = 128, SKINNY_LAUNCH_COLS = 64;
+static bool skinny_wide(const tq_tensor *a, int64_t ncols) {
+    return a->type == TQ_TYPE_Q4_K && ncols > SKINNY_MAX_COLS && ncols <= SKINNY_WIDE_MAX_COLS &&
+           a->ne[1] < SKINNY_BIG_ROWS;
+}
 static bool use_skinny(const tq_tensor *a, int64_t ncols, int nb, bool f32) {
     if (skinny_big(a) && ncols >= 3 && ncols <= 4) return true;
+    if (skinny_wide(a, ncols)) return true;
     if (f32 && ncols <= 4 && ncols * nb <= 32) return false;
     return skinny_columns(a->type, ncols);
 }
 
-// Q6_K at K = 2048 or 4096 from 3 to 32 columns (2 on matrices of 64K rows and more): the Q6_K MFMA
-// kernel, 16 (K = 2048) or 8 columns per launch, F32 activations of up to 8 columns quantized inside it
-// (more get the Q8_K pass: every workgroup would repeat it); from 33 columns the prefill kernel. On MI355X, ops on F32 columns
+// Q6_K at K = 2048 or 4096 from 3 to 32 columns (2 on matrices of 64K rows and more; below them up to
+// 64 at K = 2048, 48 at K = 4096): the Q6_K MFMA kernel, 16 (K = 2048) or 8 columns per launch, F32
+// activations of up to 8 columns quantized inside it (more get the Q8_K pass: every workgroup would
+// repeat it); above that the prefill kernel (2048 x 4096 at 33 / 64 columns 22.0 / 32.3 us, 49.7 / 51.4
+// on the prefill kernel, which takes 65 in 38.6; on the 151936-row head the prefill kernel is as fast
+// from 33 columns: 185-192 us). On MI355X, ops on F32 columns
 // in graphs, against the GEMV: the 151936 x 2048 head at 2 / 3 / 4 / 8 columns 45.0 / 43.5 / 44.0 /
 // 53.2 us against 46.8 / 57.1 / 58.9 / 97.3; 4096 rows 5.9 / 6.2 / 6.5 / 8.9 against 5.1 / 6.4 / 6.9 /
 // 11.2; 512 rows 5.4 / 5.7 / 6.0 / 8.3 against 4.6 / 6.0 / 6.5 / 10.3. The head at 16 / 32 / 64 Q8_K
@@ -253,15 +265,20 @@ static GemvArgs weight_args(const tq_tensor *a) {
     return g;
 }
 static bool skinny6_shape(const tq_tensor *a) { return a->type == TQ_TYPE_Q6_K && skinny_q6k_supported(weight_args(a)); }
+static int64_t skinny6_max_cols(const tq_tensor *a) {
+    if (a->ne[1] >= SKINNY6_TWO_COL_MIN_ROWS) return SKINNY6_MAX_COLS;
+    return a->ne[0] == 2 * QK * 8 ? 48 : 64;  // K = 4096 (8 columns per launch): 4096 x 2048 at 48 / 64 columns
+                                               // 64.1 / 84.3 us, the prefill kernel 70.9 at 65
+}
 static bool use_skinny6(const tq_tensor *a, int64_t ncols) {
     const bool cols = (ncols >= SKINNY6_MIN_COLS || (ncols == 2 && a->ne[1] >= SKINNY6_TWO_COL_MIN_ROWS)) &&
-                      ncols <= SKINNY6_MAX_COLS;
+                      ncols <= skinny6_max_cols(a);
     return cols && skinny6_shape(a);
 }
 
 static bool use_mmq(const tq_tensor *a, int64_t ncols) {
-    const int64_t min_cols = ncols > SKINNY6_MAX_COLS && skinny6_shape(a) ? SKINNY6_MAX_COLS + 1 : MMQ_MIN_COLS;
-    return ncols >= min_cols && !skinny_columns(a->type, ncols) && !use_skinny6(a, ncols);
+    const int64_t min_cols = ncols > skinny6_max_cols(a) && skinny6_shape(a) ? skinny6_max_cols(a) + 1 : MMQ_MIN_COLS;
+    return ncols >= min_cols && !skinny_columns(a->type, ncols) && !use_skinny6(a, ncols) && !skinny_wide(a, ncols);
 }
 
 // Decode-size F32 activations are quantized inside the GEMV workgroups (no workspace, one launch): up
@@ -444,7 +461,19 @@ int tq_mul_mat(const tq_tensor *a, const tq_tensor *b, tq_tensor *dst, void *wor
                 m.arrivals = sc->tiles;
             }
         }
-        if (skinny) return check_hip(launch_skinny(a->type, m, s), "skinny launch");
+        if (skinny) {
+            // up to 64 columns per launch (more below 16K rows), each launch on its part of the Q8_K columns
+            const int64_t ncol = b->ne[1];
+            m.q8_cols = (int32_t)ncol;
+            for (int64_t c0 = 0; c0 < ncol; c0 += SKINNY_LAUNCH_COLS) {
+                MmqArgs mc = m;
+                mc.q8 = (const uint8_t *)q8 + c0 * nb * Q8K_BYTES;
+                mc.dst = (float *)dst->data + c0 * mc.d_s1;
+                mc.ncols = (int32_t)std::min<int64_t>(SKINNY_LAUNCH_COLS, ncol - c0);
+                if ((rc = check_hip(launch_skinny(a->type, mc, s), "skinny launch"))) return rc;
+            }
+            return TQ_STATUS_SUCCESS;
+        }
         return check_hip(launch_mmq(a->type, m, s), "mmq launch");
     }
     GemvArgs g = weight_args(a);

@@ -80,6 +80,7 @@ struct MmqArgs {
     int32_t ksplit;      // tile kernels: workgroups per output tile along k (1: none)
     float *part;         // ksplit > 1: workspace of mmq_split_bytes for the partial tiles
     unsigned *arrivals;  // ksplit > 1: the tiles' arrival counts (the stream's SyncCounters::tiles)
+    int32_t q8_cols;     // skinny kernels: columns per batch in q8 when a launch takes a part of them (0: ncols)
 };
 hipError_t launch_mmq(int type, const MmqArgs &a, hipStream_t stream);
 // The large-tile prefill kernel (128 x 256 tiles, LDS-DMA staging); launch_mmq takes it when supported.

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k(SkinnyArgs a) {
     const int nb = a.nb, rp = 9 * nb;
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
     const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
-    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * a.ncols * nb * Q8K_BYTES;
+    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * (a.q8_cols ? a.q8_cols : a.ncols) * nb * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
     const int64_t r0 = (int64_t)blockIdx.x * 16, row = r0 + n;
     const bool rv = row < a.nrows;
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_skinny_q4k_direct(SkinnyArgs 
     const int nb = a.nb;
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
     const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
-    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * a.ncols * nb * Q8K_BYTES;
+    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * (a.q8_cols ? a.q8_cols : a.ncols) * nb * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
     const int64_t row = (int64_t)blockIdx.x * 16 + n;
     const bool rv = row < a.nrows;
@@ -479,7 +479,7 @@ void k_skinny_q4k_p(SkinnyArgs a) {
     const int n = lane & 15, g = lane >> 4;
     const int i2 = blockIdx.y % a.ne12, i3 = blockIdx.y / a.ne12;
     const uint8_t *w = a.w + (int64_t)(i2 / a.r2) * a.w_s2 + (int64_t)(i3 / a.r3) * a.w_s3;
-    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * a.ncols * NB * Q8K_BYTES;
+    const uint8_t *q8 = a.q8 + (int64_t)blockIdx.y * (a.q8_cols ? a.q8_cols : a.ncols) * NB * Q8K_BYTES;
     float *dst = a.dst + i2 * a.d_s2 + i3 * a.d_s3;
     const int ncols = a.ncols;  // 1 .. 16 MT
     const int64_t ntiles = (a.nrows + 15) / 16;
