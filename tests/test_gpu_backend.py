@@ -53,7 +53,7 @@ def layer(gpu, T):
     return nodes, W, (gate, up, down, gate_inp, norm, x, attn)
 
 
-@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("T", [1, 4, 16])
 def test_decode_layer_through_the_backend(gpu, T):
     _case(f"layer T={T}")
     assert B.Backend.gpu_count() >= 1
@@ -107,6 +107,37 @@ def test_backend_compute_in_a_graph(gpu):
         for n, ref in zip(nodes, eager):
             for t, r in zip(n.dsts, ref):
                 assert torch.equal(t, r), f"replay {rep}: node op {n.op} differs from the eager compute"
+    be.close()
+
+
+@pytest.mark.parametrize("T", [8, 16, 40])
+def test_backend_shared_q8_pass(gpu, T):
+    """Consecutive MUL_MAT nodes on one F32 b share one Q8_K pass (q/k/v at 8, 16 and 40 columns, where
+    each call alone would quantize b itself), bit for bit the separate calls. A node that writes its
+    output over b ends the run: the node after it reads the new b, as in node order."""
+    _case(f"shared q8 pass T={T}")
+    be = B.Backend.gpu(0)
+    wq, wk, wv = (make_weights(ggml.Type.Q4_K, 2048, n, 30 + n, gpu) for n in (4096, 512, 512))
+    wsq = make_weights(ggml.Type.Q4_K, 2048, 2048, 31, gpu)
+    w6 = make_weights(ggml.Type.Q6_K, 2048, 1000, 32, gpu)
+    x = torch.from_numpy(normal((T, 2048), 33 + T)).to(gpu)
+    x0 = x.clone()
+    nodes = [B.mul_mat(wq, x), B.mul_mat(wk, x), B.mul_mat(w6, x), B.mul_mat(wv, x),
+             B.mul_mat(wsq, x, out=x),  # writes over b
+             B.mul_mat(wk, x), B.mul_mat(wv, x)]
+    be.reserve(nodes)
+    be.compute_async(nodes)
+    be.synchronize()
+    torch.cuda.synchronize()
+    for n, w in zip(nodes[:4], (wq, wk, w6, wv)):
+        assert torch.equal(n.out, ggml.mul_mat(w, x0)), "shared-pass node differs from tq_mul_mat"
+    x1 = ggml.mul_mat(wsq, x0)
+    assert torch.equal(x, x1)
+    for n, w in zip(nodes[5:], (wk, wv)):
+        assert torch.equal(n.out, ggml.mul_mat(w, x1)), "node after the overwrite did not read the new b"
+    want = O.mul_mat(wq.type.id, wq.data.cpu().numpy(), 2048, 4096, x0.cpu().numpy())[0]
+    got = nodes[0].out.cpu().numpy()
+    assert float(np.abs(got - want).max() / np.abs(want).max()) <= 1e-3
     be.close()
 
 

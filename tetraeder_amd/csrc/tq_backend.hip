@@ -14,6 +14,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace {
@@ -61,6 +62,37 @@ size_t node_workspace(const tq_node &n) {
     case TQ_NODE_MOE_FFN_SUM: return tq_moe_ffn_workspace_size(n.src[0], n.src[3], n.src[4]);
     default: return 0;
     }
+}
+
+// The bytes of the Q8_K pass tq_mul_mat would run on a MUL_MAT node's F32 b (0: none, the b is quantized
+// inside the kernel or is Q8_K already): its workspace with b in F32 less its workspace with b in Q8_K.
+tq_tensor q8_view(const tq_tensor &b, void *data) {
+    tq_tensor q = b;
+    const size_t rs = (size_t)(b.ne[0] / tq::QK) * tq::Q8K_BYTES;
+    q.type = TQ_TYPE_Q8_K;
+    q.nb[0] = tq::Q8K_BYTES, q.nb[1] = rs, q.nb[2] = rs * b.ne[1], q.nb[3] = rs * b.ne[1] * b.ne[2];
+    q.data = data;
+    return q;
+}
+size_t q8_pass_bytes(const tq_node &n) {
+    if (n.op != TQ_NODE_MUL_MAT || n.src[1]->type != TQ_TYPE_F32 || n.src[1]->ne[0] % tq::QK) return 0;
+    const tq_tensor q = q8_view(*n.src[1], nullptr);
+    const size_t f32 = tq_mul_mat_workspace_size(n.src[0], n.src[1]), q8 = tq_mul_mat_workspace_size(n.src[0], &q);
+    return f32 > q8 ? f32 - q8 : 0;
+}
+bool same_tensor(const tq_tensor &x, const tq_tensor &y) {
+    return x.type == y.type && x.data == y.data && std::equal(x.ne, x.ne + 4, y.ne) && std::equal(x.nb, x.nb + 4, y.nb);
+}
+// [first, last) byte span of a tensor's elements
+std::pair<uintptr_t, uintptr_t> span(const tq_tensor &t) {
+    size_t ext = 0;
+    for (int d = 1; d < 4; ++d) ext += (size_t)(t.ne[d] > 0 ? t.ne[d] - 1 : 0) * t.nb[d];
+    const size_t row = t.type == TQ_TYPE_F32 || t.type == TQ_TYPE_I32 ? (size_t)t.ne[0] * 4 : t.nb[1];
+    return {(uintptr_t)t.data, (uintptr_t)t.data + ext + row};
+}
+bool overlaps(const tq_tensor &x, const tq_tensor &y) {
+    const auto a = span(x), b = span(y);
+    return a.first < b.second && b.first < a.second;
 }
 
 }  // namespace
@@ -185,6 +217,35 @@ int tq_backend_graph_compute(tq_backend *b, const tq_node *nodes, int n_nodes) {
         void *ws = b->arena;
         const size_t wsz = b->arena_size;
         int rc;
+        // Consecutive MUL_MAT nodes on the same F32 b (the attention projections q/k/v) share one Q8_K
+        // pass when each would run one: the Q8_K rows go to the front of the arena, the nodes' own
+        // workspace after them (a node's F32 workspace is those rows plus its own part, so the reserve
+        // covers this). The run ends before a node that does not fit the arena, or after one whose dst
+        // overlaps b (the next node reads what that one wrote). The kernels are those of the separate
+        // calls, on the same Q8_K bytes, so the outputs are bit for bit theirs.
+        const size_t q8 = q8_pass_bytes(n);
+        int end = k + 1;
+        if (q8)
+            while (end < n_nodes && nodes[end].op == TQ_NODE_MUL_MAT && same_tensor(*nodes[end].src[1], *n.src[1]) &&
+                   q8_pass_bytes(nodes[end]) == q8 && node_workspace(nodes[end]) <= b->arena_size &&
+                   !overlaps(*nodes[end - 1].dst[0], *n.src[1]))
+                ++end;
+        if (end - k > 1) {
+            const tq_tensor bq = q8_view(*n.src[1], ws);
+            if ((rc = tq_quantize_q8_K(n.src[1], ws, s)) != TQ_STATUS_SUCCESS) {
+                const std::string why = tq_last_error();
+                return tq::fail(rc, "node %d (op %d): %s", k, n.op, why.c_str());
+            }
+            for (int j = k; j < end; ++j) {
+                const tq_node &m = nodes[j];
+                if ((rc = tq_mul_mat(m.src[0], &bq, m.dst[0], (uint8_t *)ws + q8, wsz - q8, s)) != TQ_STATUS_SUCCESS) {
+                    const std::string why = tq_last_error();
+                    return tq::fail(rc, "node %d (op %d): %s", j, m.op, why.c_str());
+                }
+            }
+            k = end - 1;
+            continue;
+        }
         switch (n.op) {
         case TQ_NODE_MUL_MAT: rc = tq_mul_mat(n.src[0], n.src[1], n.dst[0], ws, wsz, s); break;
         case TQ_NODE_MUL_MAT_ID: rc = tq_mul_mat_id(n.src[0], n.src[1], n.src[2], n.dst[0], ws, wsz, s); break;
