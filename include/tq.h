@@ -276,9 +276,10 @@ int tq_backend_reserve(tq_backend *backend, const tq_node *nodes, int n_nodes);
 /* Runs the nodes in order on the backend's stream (asynchronous; no host synchronization, no
  * allocation: a node needing more workspace than the last reserve provided fails with -1 before
  * anything of it is issued). Returns the ggml_status of the first node that fails, with its index in
- * tq_last_error(). ggml_backend_graph_compute_async. Consecutive MUL_MAT nodes on the same F32 b that
- * would each quantize it to Q8_K share one such pass (up to a node whose dst overlaps b); their outputs
- * are bit for bit those of separate tq_mul_mat calls. */
+ * tq_last_error(). ggml_backend_graph_compute_async. Consecutive MUL_MAT nodes on the same F32 b share
+ * one Q8_K pass where each would quantize b itself and where 4 and more Q4_K columns then run on the
+ * MFMA kernel (up to a node whose dst overlaps b); each output is bit for bit that of tq_mul_mat on the
+ * Q8_K rows of b (tq_quantize_q8_K). */
 int tq_backend_graph_compute(tq_backend *backend, const tq_node *nodes, int n_nodes);
 
 /* Waits for the backend's stream (ggml_backend_synchronize). */

@@ -24,6 +24,11 @@ def _case(name):
     print(f"[backend] {name}", file=sys.stderr, flush=True)
 
 
+def q8(x):
+    """x [m, k] float32 as the Q8_K tensor tq_quantize_q8_K makes of it."""
+    return ggml.QTensor(ggml.Type.Q8_K, (x.shape[-1], x.shape[0]), ggml.quantize_q8_K(x).view(-1))
+
+
 def make_weights(ty, k, n, seed, device):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
@@ -68,8 +73,10 @@ def test_decode_layer_through_the_backend(gpu, T):
     nq, nk, nv, no, nr, nm, nh = nodes
     # each node against its entry point called alone, on the node's own inputs
     torch.cuda.synchronize()
+    # (q/k/v share one Q8_K pass from 4 columns: each equals tq_mul_mat on the Q8_K rows of x)
     for n, w, inp in ((nq, W["q"], x), (nk, W["k"], x), (nv, W["v"], x), (no, W["o"], attn), (nh, W["head"], nm.out)):
-        assert torch.equal(n.out, ggml.mul_mat(w, inp)), "MUL_MAT node differs from tq_mul_mat"
+        ref = ggml.mul_mat(w, q8(inp) if inp is x and T >= 4 else inp).reshape(n.out.shape)
+        assert torch.equal(n.out, ref), "MUL_MAT node differs from tq_mul_mat"
     xn, wts, ids = ggml.moe_router(no.out, norm, gate_inp, 1e-6, 8)
     assert torch.equal(nr.out[0], xn) and torch.equal(nr.out[1], wts) and torch.equal(nr.out[2], ids)
     y = ggml.moe_ffn_sum(gate, up, down, nr.out[0].view(T, 1, -1), nr.out[2], nr.out[1])
@@ -82,11 +89,12 @@ def test_decode_layer_through_the_backend(gpu, T):
     be.close()
 
 
-def test_backend_compute_in_a_graph(gpu):
+@pytest.mark.parametrize("T", [2, 16])
+def test_backend_compute_in_a_graph(gpu, T):
     """A reserved compute records into a HIP graph (nothing allocated, no host synchronization); three
-    replays, with the outputs poisoned and other work on the stream between them, equal the eager run."""
-    _case("graph capture")
-    T = 2
+    replays, with the outputs poisoned and other work on the stream between them, equal the eager run
+    (at 16 columns q/k/v share one Q8_K pass)."""
+    _case(f"graph capture T={T}")
     nodes, W, _ = layer(gpu, T)
     be = B.Backend.gpu(0)
     be.reserve(nodes)
@@ -110,11 +118,12 @@ def test_backend_compute_in_a_graph(gpu):
     be.close()
 
 
-@pytest.mark.parametrize("T", [8, 16, 40])
+@pytest.mark.parametrize("T", [2, 4, 8, 16, 40])
 def test_backend_shared_q8_pass(gpu, T):
-    """Consecutive MUL_MAT nodes on one F32 b share one Q8_K pass (q/k/v at 8, 16 and 40 columns, where
-    each call alone would quantize b itself), bit for bit the separate calls. A node that writes its
-    output over b ends the run: the node after it reads the new b, as in node order."""
+    """Consecutive MUL_MAT nodes on one F32 b share one Q8_K pass (Q4_K from 4 columns, Q6_K from 9),
+    each bit for bit tq_mul_mat on the Q8_K rows of b; at 2 columns and for the Q6_K node up to 8 the
+    nodes run alone, bit for bit tq_mul_mat on the F32 b. A node that writes its output over b ends the
+    run: the nodes after it read the new b, as in node order."""
     _case(f"shared q8 pass T={T}")
     be = B.Backend.gpu(0)
     wq, wk, wv = (make_weights(ggml.Type.Q4_K, 2048, n, 30 + n, gpu) for n in (4096, 512, 512))
@@ -129,12 +138,16 @@ def test_backend_shared_q8_pass(gpu, T):
     be.compute_async(nodes)
     be.synchronize()
     torch.cuda.synchronize()
+    def ref(w, b):
+        shared = T >= 9 or (T >= 4 and w.type == ggml.Type.Q4_K)
+        return ggml.mul_mat(w, q8(b) if shared else b).reshape(b.shape[0], w.ne[1])
+
     for n, w in zip(nodes[:4], (wq, wk, w6, wv)):
-        assert torch.equal(n.out, ggml.mul_mat(w, x0)), "shared-pass node differs from tq_mul_mat"
-    x1 = ggml.mul_mat(wsq, x0)
+        assert torch.equal(n.out, ref(w, x0)), "node differs from tq_mul_mat"
+    x1 = ref(wsq, x0)
     assert torch.equal(x, x1)
     for n, w in zip(nodes[5:], (wk, wv)):
-        assert torch.equal(n.out, ggml.mul_mat(w, x1)), "node after the overwrite did not read the new b"
+        assert torch.equal(n.out, ref(w, x1)), "node after the overwrite did not read the new b"
     want = O.mul_mat(wq.type.id, wq.data.cpu().numpy(), 2048, 4096, x0.cpu().numpy())[0]
     got = nodes[0].out.cpu().numpy()
     assert float(np.abs(got - want).max() / np.abs(want).max()) <= 1e-3

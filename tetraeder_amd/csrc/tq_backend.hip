@@ -52,10 +52,19 @@ struct DeviceScope {
     }
 };
 
-// The bytes of workspace one node needs (its entry point's *_workspace_size).
+tq_tensor q8_view(const tq_tensor &b, void *data);
+size_t q8_pass_bytes(const tq_node &n);
+
+// The bytes of workspace one node needs (its entry point's *_workspace_size; for a MUL_MAT whose F32 b
+// may be quantized once for a run of nodes, at least those Q8_K rows and its workspace on them).
 size_t node_workspace(const tq_node &n) {
     switch (n.op) {
-    case TQ_NODE_MUL_MAT: return tq_mul_mat_workspace_size(n.src[0], n.src[1]);
+    case TQ_NODE_MUL_MAT: {
+        const size_t own = tq_mul_mat_workspace_size(n.src[0], n.src[1]), q8 = q8_pass_bytes(n);
+        if (!q8) return own;
+        const tq_tensor bq = q8_view(*n.src[1], nullptr);
+        return std::max(own, q8 + tq_mul_mat_workspace_size(n.src[0], &bq));
+    }
     case TQ_NODE_MUL_MAT_ID: return tq_mul_mat_id_workspace_size(n.src[0], n.src[1], n.src[2]);
     case TQ_NODE_MOE_ROUTER: return tq_moe_router_workspace_size(n.src[2], n.src[0]);
     case TQ_NODE_MOE_FFN:
@@ -64,8 +73,7 @@ size_t node_workspace(const tq_node &n) {
     }
 }
 
-// The bytes of the Q8_K pass tq_mul_mat would run on a MUL_MAT node's F32 b (0: none, the b is quantized
-// inside the kernel or is Q8_K already): its workspace with b in F32 less its workspace with b in Q8_K.
+// A MUL_MAT node's b as contiguous Q8_K rows at data.
 tq_tensor q8_view(const tq_tensor &b, void *data) {
     tq_tensor q = b;
     const size_t rs = (size_t)(b.ne[0] / tq::QK) * tq::Q8K_BYTES;
@@ -74,11 +82,9 @@ tq_tensor q8_view(const tq_tensor &b, void *data) {
     q.data = data;
     return q;
 }
+// The Q8_K bytes of a MUL_MAT node's b when nodes sharing it quantize it once (0: the node runs alone).
 size_t q8_pass_bytes(const tq_node &n) {
-    if (n.op != TQ_NODE_MUL_MAT || n.src[1]->type != TQ_TYPE_F32 || n.src[1]->ne[0] % tq::QK) return 0;
-    const tq_tensor q = q8_view(*n.src[1], nullptr);
-    const size_t f32 = tq_mul_mat_workspace_size(n.src[0], n.src[1]), q8 = tq_mul_mat_workspace_size(n.src[0], &q);
-    return f32 > q8 ? f32 - q8 : 0;
+    return n.op == TQ_NODE_MUL_MAT ? tq::mul_mat_shared_q8_bytes(n.src[0], n.src[1]) : 0;
 }
 bool same_tensor(const tq_tensor &x, const tq_tensor &y) {
     return x.type == y.type && x.data == y.data && std::equal(x.ne, x.ne + 4, y.ne) && std::equal(x.nb, x.nb + 4, y.nb);
@@ -218,11 +224,10 @@ int tq_backend_graph_compute(tq_backend *b, const tq_node *nodes, int n_nodes) {
         const size_t wsz = b->arena_size;
         int rc;
         // Consecutive MUL_MAT nodes on the same F32 b (the attention projections q/k/v) share one Q8_K
-        // pass when each would run one: the Q8_K rows go to the front of the arena, the nodes' own
-        // workspace after them (a node's F32 workspace is those rows plus its own part, so the reserve
-        // covers this). The run ends before a node that does not fit the arena, or after one whose dst
-        // overlaps b (the next node reads what that one wrote). The kernels are those of the separate
-        // calls, on the same Q8_K bytes, so the outputs are bit for bit theirs.
+        // pass where that pays (tq::mul_mat_shared_q8_bytes): the Q8_K rows go to the front of the
+        // arena, the nodes' own workspace after them (node_workspace counts both). The run ends before a
+        // node that does not fit the arena, or after one whose dst overlaps b (the next node reads what
+        // that one wrote). Each node's output is bit for bit that of tq_mul_mat on the Q8_K rows of b.
         const size_t q8 = q8_pass_bytes(n);
         int end = k + 1;
         if (q8)

@@ -7,10 +7,16 @@
 #include <stddef.h>
 #include <stdint.h>
 
+struct tq_tensor;
+
 namespace tq {
 
 // Records the message of a failed call for tq_last_error() (this host thread) and returns code.
 int fail(int code, const char *fmt, ...);
+
+// The Q8_K bytes of an F32 b that MUL_MAT nodes sharing it should quantize once (tq_backend.hip), 0 when
+// a node on it is better off on its own (tq_api.hip).
+size_t mul_mat_shared_q8_bytes(const tq_tensor *a, const tq_tensor *b);
 
 // Counters of the kernels whose workgroups count or wait for each other: the k split's tile arrivals,
 // the router's token arrivals and the MoE step's phase counts. Each stream that issues such a call gets
