@@ -82,9 +82,10 @@ tq_tensor q8_view(const tq_tensor &b, void *data) {
     q.data = data;
     return q;
 }
-// The Q8_K bytes of a MUL_MAT node's b when nodes sharing it quantize it once (0: the node runs alone).
+// The Q8_K bytes of a MUL_MAT node's b when nodes sharing it quantize it once (0: the node runs alone,
+// as does one with a missing operand, which its own call then refuses).
 size_t q8_pass_bytes(const tq_node &n) {
-    return n.op == TQ_NODE_MUL_MAT ? tq::mul_mat_shared_q8_bytes(n.src[0], n.src[1]) : 0;
+    return n.op == TQ_NODE_MUL_MAT && n.src[0] && n.src[1] && n.dst[0] ? tq::mul_mat_shared_q8_bytes(n.src[0], n.src[1]) : 0;
 }
 bool same_tensor(const tq_tensor &x, const tq_tensor &y) {
     return x.type == y.type && x.data == y.data && std::equal(x.ne, x.ne + 4, y.ne) && std::equal(x.nb, x.nb + 4, y.nb);
@@ -231,8 +232,8 @@ int tq_backend_graph_compute(tq_backend *b, const tq_node *nodes, int n_nodes) {
         const size_t q8 = q8_pass_bytes(n);
         int end = k + 1;
         if (q8)
-            while (end < n_nodes && nodes[end].op == TQ_NODE_MUL_MAT && same_tensor(*nodes[end].src[1], *n.src[1]) &&
-                   q8_pass_bytes(nodes[end]) == q8 && node_workspace(nodes[end]) <= b->arena_size &&
+            while (end < n_nodes && q8_pass_bytes(nodes[end]) == q8 && same_tensor(*nodes[end].src[1], *n.src[1]) &&
+                   node_workspace(nodes[end]) <= b->arena_size &&
                    !overlaps(*nodes[end - 1].dst[0], *n.src[1]))
                 ++end;
         if (end - k > 1) {
