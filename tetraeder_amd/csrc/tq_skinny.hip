@@ -1,7 +1,8 @@
 // tq_skinny.hip -- MUL_MAT for a few activation columns (batched decode) on int8 MFMA
-// (v_mfma_i32_16x16x64_i8), every weight byte read once for all columns: Q4_K at 4..64 columns (one
-// workgroup per 16-row tile, or persistent workgroups over tile ranges on large matrices) and Q6_K at
-// K = 2048 / 4096 (persistent). The operand layouts and the super-block steps are in tq_skinny.h.
+// (v_mfma_i32_16x16x64_i8), every weight byte read once for all columns of a launch: Q4_K at up to 64
+// columns a launch (one workgroup per 16-row tile, or persistent workgroups over tile ranges on large
+// matrices; a launch may take a part of the Q8_K columns, whose batch stride is then q8_cols) and Q6_K
+// at K = 2048 / 4096 (persistent). The operand layouts and the super-block steps are in tq_skinny.h.
 // The waves of a workgroup split the super-blocks of a tile and their partial sums meet in LDS.
 #include "tq_device.h"
 #include "tq_internal.h"
