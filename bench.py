@@ -15,8 +15,9 @@ that profile was taken on the sources this run was built from (their hash is com
 cpu_baseline: the restated iqk AVX-512 VNNI CPU path (oracle/tq_cpu_baseline.c) on the host cores,
 same weight bytes, Q8_K quantization included, weight copies rotated; cpu_baselines: one line per
 workload (Q4_K 4096 x 4096, Q6_K head, attention projections, the MoE MUL_MAT_ID step, prefill).
-secondary: the other workloads (Q6_K head at batch 1 and 4, attention projections, MUL_MAT_ID at
-prefill sizes and its expert-parallel rank shares, the MoE step and router, prefill, slot uploads).
+secondary: the other workloads (Q6_K head at batch 1 and 4, attention projections, q/k/v as backend
+nodes sharing one Q8_K pass, MUL_MAT_ID at prefill sizes and its expert-parallel rank shares, the MoE
+step and router, prefill, slot uploads).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -660,6 +661,51 @@ def bench_secondary(ggml, torch, dev):
             res[f"attn_{name}_proj_{k}x{n}_m{m}"] = {"op_us": round(us, 2), "GBps": round(wb / us / 1e3, 1)}
         del W
         log(f"attn {name}: " + ", ".join(f"m{m} {res[f'attn_{name}_proj_{k}x{n}_m{m}']['op_us']}us" for m in (1, 4, 16, 32)))
+    torch.cuda.empty_cache()
+    # q, k, v of one layer as a run of backend nodes (one Q8_K pass shared from 4 columns) against three
+    # separate calls; 48 rotated layer copies (288 MB, past the MALL), graphs on the backend's stream
+    from tetraeder_amd import backend as B
+    copies = 48
+    Wl = [[make_weights(ggml, torch, ty, 2048, n, 1, seed=c * 3 + j, dev=dev)[0] for j, n in enumerate((4096, 512, 512))]
+          for c in range(copies)]
+    stream = torch.cuda.Stream()
+    be = B.Backend.gpu(0, stream=stream)
+    qkv = {}
+    for m in (1, 4, 16, 32):
+        x = torch.randn((m, 2048), device=dev)
+        lists = [[B.mul_mat(w, x) for w in Wl[c]] for c in range(copies)]
+        be.reserve([nd for l in lists for nd in l])
+        for l in lists:
+            be.compute_async(l)
+        be.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for l in lists:
+                be.compute_async(l)
+        outs = [[nd.out for nd in l] for l in lists]
+        ws = torch.empty(max(1, max(ggml.mul_mat_workspace_size(w, x) for w in Wl[0])), dtype=torch.uint8, device=dev)
+
+        def sep(i):
+            for w, o in zip(Wl[i % copies], outs[i % copies]):
+                ggml.mul_mat(w, x, out=o, workspace=ws)
+
+        t_sep = time_graph(torch, sep, copies)
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for _ in range(20):
+                g.replay()
+            t1.record(stream)
+            t1.synchronize()
+        t_be = t0.elapsed_time(t1) * 1e3 / (20 * copies)
+        qkv[f"m{m}"] = {"backend_us": round(t_be, 2), "separate_calls_us": round(t_sep, 2)}
+        del g, lists, outs
+    be.close()
+    res["attn_qkv_2048x4096_512_512_backend"] = qkv
+    log(f"attn qkv backend vs separate calls: {qkv}")
+    del Wl
     torch.cuda.empty_cache()
     # MUL_MAT_ID at prefill sizes: gate Q4_K [2048 -> 768] x 128 experts, top-8 of 512 and 2048 tokens
     E, k, n = 128, 2048, 768
